@@ -1,0 +1,193 @@
+#!/usr/bin/env python3
+"""Decode-step benchmark of the MI355X GQA flash-decode path.
+
+A step is one decode call over one batch (default: the headline workload M0,
+paged fp16 KV, B=4, Hq=32, Hkv=8, D=128, 32768 tokens per sequence, 16-token
+pages scattered by a seeded permutation).  Inputs are generated on the GPU and
+are resident in HBM before timing; several independent input sets are rotated
+so the working set exceeds the 256 MB Infinity Cache.
+
+Prints one JSON line.  ``value`` is the achieved algorithmic HBM bandwidth of a
+whole step (valid K+V bytes + Q + output + block-table entries + lengths) in
+GB/s; ``us_per_step`` and ``pct_of_peak`` (of 8 TB/s) are reported beside it.
+``roofline`` is the split-KV partial kernel alone, timed with HIP events on
+the launch stream over the timed region.  ``cpu_baseline`` times the CPU
+oracle on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "µs/step + achieved HBM GB/s (% peak), paged GQA decode B=4 Hq32/Hkv8 D128 32K"
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="M0", help="workload name (M0, C1..C5)")
+    ap.add_argument("--sets", type=int, default=0, help="input sets to rotate (0: enough for >1 GB)")
+    ap.add_argument("--chunk", type=int, default=0, help="split size in tokens (0: library default)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                      "profiles", "traffic_M0.json"),
+                    help="JSON with rocprof-derived HBM bytes per partial-kernel launch")
+    return ap.parse_args()
+
+
+def cpu_baseline(wl, budget_s: float):
+    """Times the numpy oracle on the first sequence of ``wl`` (bounded sample)."""
+    import numpy as np
+    import torch
+
+    from oracle import decode_oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover - threadpoolctl missing
+        threads = 1
+    L = wl.lens[0]
+    q = wl.q[:1].float().cpu().numpy()
+    if wl.layout == "paged":
+        npg = (L + 15) // 16
+        pages = wl.block_table[0, :npg].long()
+        k = wl.k[pages].cpu()
+        v = wl.v[pages].cpu()
+        bt = np.arange(npg, dtype=np.int64)[None, :]
+        kw = {}
+        if wl.k_scale is not None:
+            k, v = k.view(torch.uint8).numpy(), v.view(torch.uint8).numpy()
+            kw = dict(k_scale=float(wl.k_scale), v_scale=float(wl.v_scale))
+        else:
+            k, v = k.float().numpy(), v.float().numpy()
+        s_aux = None if wl.s_aux is None else wl.s_aux.cpu().numpy()
+
+        def step():
+            O.decode_paged(q, k, v, bt, [L], s_aux, "exp", **kw)
+    else:
+        k = wl.k[: L].float().cpu().numpy()
+        v = wl.v[: L].float().cpu().numpy()
+        cu = np.array([0, L])
+        s_aux = None if wl.s_aux is None else wl.s_aux.cpu().numpy()
+
+        def step():
+            O.decode_varlen(q, k, v, cu, s_aux)
+    step()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    kv_bytes = L * wl.Hkv * wl.D * 2 * wl.k.element_size()
+    sample_bytes = kv_bytes + wl.Hq * wl.D * (wl.q.element_size() + 2)
+    return {
+        "value": round(sample_bytes / med / 1e9, 4),
+        "unit": "GB/s",
+        "us_per_step_extrapolated": round(med * 1e6 * wl.B, 1),
+        "cores": threads,
+        "kind": "port",
+        "sample": f"numpy float64 oracle, sequence 0 of {wl.name} ({L} tokens, {wl.Hq} q heads), "
+                  f"median of {len(times)} runs",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only "
+                                   "(see DESIGN.md), so --gpus must be 1", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    from fasterkernels_amd import _native as nat
+    from fasterkernels_amd import workloads as W
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no HIP GPU visible"}))
+        sys.exit(2)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    base = W.make(args.config, gen_device=dev, device=dev)
+    kv_bytes = base.k.numel() * base.k.element_size() * 2
+    n_sets = args.sets or max(1, min(8, -(-1_100_000_000 // kv_bytes)))
+    sets = [base] + [W.make(args.config, gen_device=dev, device=dev, seed=base.meta["seed"] + 1000 * i)
+                     for i in range(1, n_sets)]
+    alg_bytes = base.algorithmic_bytes()
+
+    def step(i):
+        return W.run(sets[i % n_sets], chunk_tokens=args.chunk)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    nat.enable_kernel_timing(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    part_ms, tot_ms, calls = nat.kernel_timing()
+    nat.enable_kernel_timing(False)
+
+    ms_step = elapsed * 1e3 / args.steps
+    gbs = alg_bytes / (ms_step / 1e3) / 1e9
+    part_avg_ms = part_ms / max(calls, 1)
+    kern_gbs = alg_bytes / (part_avg_ms / 1e3) / 1e9 if part_avg_ms > 0 else None
+    traffic = None
+    if os.path.exists(args.traffic) and args.config == "M0" and not args.chunk:
+        with open(args.traffic) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+
+    out = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "us_per_step": round(ms_step * 1e3, 2),
+        "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if base.k.dtype == torch.float16 else str(base.k.dtype).replace("torch.", ""),
+        "data": f"synthetic N(0,1), generated on device, {n_sets} rotating input sets",
+        "config": {
+            "workload": f"{args.config}: {base.layout} GQA decode B={base.B} Hq={base.Hq} Hkv={base.Hkv} "
+                        f"D={base.D} tokens={base.total_tokens} kv={str(base.k.dtype).replace('torch.', '')}",
+            "batch": base.B, "total_tokens": base.total_tokens, "algorithmic_bytes": alg_bytes,
+            "chunk_tokens": args.chunk or "auto",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": None if kern_gbs is None else round(kern_gbs, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": None if kern_gbs is None else round(kern_gbs / PEAK_HBM_GBS, 4),
+            "traffic": traffic,
+            "kernel": "partial_kernel (split-KV partials)",
+            "kernel_avg_us": round(part_avg_ms * 1e3, 3),
+            "partial_plus_reduce_avg_us": round(tot_ms / max(calls, 1) * 1e3, 3),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(sets[0], args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

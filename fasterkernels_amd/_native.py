@@ -1,0 +1,130 @@
+"""ctypes binding of libfsk_decode.so (the C ABI in include/fsk_decode.h).
+
+The library is built in-tree by ``python -m fasterkernels_amd.build``.  Nothing
+here falls back to another implementation: if the library is missing, every
+decode entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfsk_decode.so")
+
+# Status codes and enums (mirrors include/fsk_decode.h).
+FSK_OK = 0
+FSK_ERR_INVALID = -1
+FSK_ERR_UNSUPPORTED = -2
+FSK_ERR_WORKSPACE = -3
+FSK_ERR_HIP = -4
+
+FSK_F16, FSK_BF16, FSK_F32, FSK_E4M3 = 0, 1, 2, 3
+FSK_SINK_EXP, FSK_SINK_LINEAR = 0, 1
+FSK_LAYOUT_VARLEN, FSK_LAYOUT_PAGED, FSK_LAYOUT_DENSE = 0, 1, 2
+
+DTYPE_CODES = {
+    torch.float16: FSK_F16,
+    torch.bfloat16: FSK_BF16,
+    torch.float32: FSK_F32,
+    torch.float8_e4m3fn: FSK_E4M3,
+}
+SINK_MODES = {"exp": FSK_SINK_EXP, "linear": FSK_SINK_LINEAR}
+
+# Every exported symbol of the C ABI, with its ctypes signature.
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+SIGNATURES = {
+    "fsk_last_error": (ctypes.c_char_p, []),
+    "fsk_version": (_I, []),
+    "fsk_set_option": (_I, [ctypes.c_char_p, _L]),
+    "fsk_workspace_bytes": (_L, [_I, _I, _I, _I, _I, _L, _I, _I]),
+    "fsk_decode_varlen": (_I, [_P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P, _P,
+                               _P, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _P, _L, _I, _P]),
+    "fsk_decode_paged": (_I, [_P, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _I, _P, _I, _I,
+                              _P, _I, _P, _P, _P, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _P, _L,
+                              _I, _P]),
+    "fsk_decode_dense": (_I, [_P, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _L, _P, _P, _P, _I, _P,
+                              _P, _P, _P, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _P, _L, _I, _P]),
+    "fsk_paged_gather": (_I, [_P, _L, _L, _L, _P, _L, _I, _P, _I, _I, _I, _I, _I, _I, _P, _P]),
+    "fsk_fp8_decode_table": (_I, [_P, _P]),
+    "fsk_enable_kernel_timing": (_I, [_I]),
+    "fsk_kernel_timing": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                               ctypes.POINTER(ctypes.c_int64)]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class FskError(RuntimeError):
+    """A HIP-side failure reported by libfsk_decode."""
+
+
+def load() -> ctypes.CDLL:
+    """Loads the library once and declares every entry point's signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"{LIB_PATH} is not built; run `python -m fasterkernels_amd.build` "
+                    "(the HIP library is required, there is no fallback)")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(status: int) -> None:
+    """Maps a library status to the Python exception the reference would raise."""
+    if status == FSK_OK:
+        return
+    msg = load().fsk_last_error().decode(errors="replace")
+    if status == FSK_ERR_INVALID:
+        raise ValueError(msg)
+    if status == FSK_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    if status == FSK_ERR_WORKSPACE:
+        raise RuntimeError(msg)
+    raise FskError(f"libfsk_decode status {status}: {msg}")
+
+
+def set_option(name: str, value: int) -> None:
+    check(load().fsk_set_option(name.encode(), int(value)))
+
+
+def workspace_bytes(layout: int, batch: int, hq: int, hkv: int, d: int, kv_extent: int,
+                    page_size: int = 16, chunk_tokens: int = 0) -> int:
+    n = load().fsk_workspace_bytes(layout, batch, hq, hkv, d, kv_extent, page_size, chunk_tokens)
+    if n < 0:
+        check(int(n))
+    return int(n)
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def enable_kernel_timing(enable: bool = True) -> None:
+    check(load().fsk_enable_kernel_timing(1 if enable else 0))
+
+
+def kernel_timing():
+    """(partial_ms, partial_plus_reduce_ms, calls) summed since the last read."""
+    a, b, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
+    check(load().fsk_kernel_timing(ctypes.byref(a), ctypes.byref(b), ctypes.byref(n)))
+    return a.value, b.value, n.value

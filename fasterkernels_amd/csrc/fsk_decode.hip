@@ -1,0 +1,1232 @@
+// fsk_decode.hip -- split-KV GQA flash decoding for MI355X (gfx950).
+//
+// Two kernels per decode call:
+//   1. partial_kernel: a persistent grid of one-wave workgroups walks a device
+//      work list of (sequence chunk, kv head) units.  Each unit streams its
+//      chunk of K/V in 32-token tiles with 128-bit buffer loads, computes
+//      S^T = K Q^T and O^T += V^T P^T on the matrix cores
+//      (v_mfma_f32_16x16x32_{f16,bf16}), keeps the online-softmax state in the
+//      MFMA accumulator layout, and writes an fp32 partial (m, l, acc[D]) per
+//      query head.  The work list is built by every workgroup from the
+//      sequence lengths (a wave prefix scan into LDS), so the host never reads
+//      lengths back and the grid size only depends on host-known bounds.
+//   2. reduce_kernel: one wave per (sequence, query head) combines the
+//      partials with a log-sum-exp merge, folds the attention sink and writes
+//      the output in the requested dtype.
+//
+// The maths follows the reference kernels: scores s = q.k * sm_scale,
+// online softmax, P rounded to the KV compute type before P.V
+// (fskernels/triton/triton_gqa_decode.py:86-109), split partials combined as
+// in fskernels/triton/triton_gqa_decode_hf.py:103-137.  bf16 P is carried as a
+// hi+lo pair of bf16 values so that the P.V product keeps fp32-level accuracy.
+// Scores are kept in the log2 domain (scale folded with log2 e), so every
+// exponential is a single v_exp_f32.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+#include <algorithm>
+#include <cmath>
+#include <string.h>
+#include <string>
+#include <vector>
+
+#include "fsk_decode.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Types and small helpers
+// ---------------------------------------------------------------------------
+typedef _Float16 f16;
+typedef __bf16 bf16;
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+// Raw buffer resource dword 3 for gfx9-family parts (format fields unused by
+// raw dword loads).
+constexpr int kRsrcWord3 = 0x00020000;
+
+enum Layout { kVarlen = 0, kPaged = 1, kDense = 2 };
+enum Kind { kF16 = FSK_F16, kBF16 = FSK_BF16, kF32 = FSK_F32, kE4M3 = FSK_E4M3 };
+
+__device__ __forceinline__ uint32_t f2u(float x) { return __builtin_bit_cast(uint32_t, x); }
+__device__ __forceinline__ float u2f(uint32_t x) { return __builtin_bit_cast(float, x); }
+
+// Max / sum over the four lanes {l, l^16, l^32, l^48} (the four k-groups of an
+// MFMA operand) with the gfx950 permlane swaps; every lane gets the result.
+__device__ __forceinline__ float group4_max(float x) {
+  auto a = __builtin_amdgcn_permlane32_swap(f2u(x), f2u(x), false, false);
+  x = fmaxf(u2f(a[0]), u2f(a[1]));
+  auto b = __builtin_amdgcn_permlane16_swap(f2u(x), f2u(x), false, false);
+  return fmaxf(u2f(b[0]), u2f(b[1]));
+}
+__device__ __forceinline__ float group4_sum(float x) {
+  auto a = __builtin_amdgcn_permlane32_swap(f2u(x), f2u(x), false, false);
+  x = u2f(a[0]) + u2f(a[1]);
+  auto b = __builtin_amdgcn_permlane16_swap(f2u(x), f2u(x), false, false);
+  return u2f(b[0]) + u2f(b[1]);
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, kWave));
+  return x;
+}
+
+// e4m3fn -> f16 / bf16, two codes per call (bytes 0,1 or 2,3 of `w`).  Both
+// conversions are exact: every e4m3 value is representable in f16 and bf16.
+template <bool kToBf16, bool kHi>
+__device__ __forceinline__ uint32_t e4m3x2_to(uint32_t w) {
+  if constexpr (kToBf16) {
+    bf16x2 h = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, kHi);
+    return __builtin_bit_cast(uint32_t, h);
+  } else {
+    f16x2 h = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, kHi);
+    return __builtin_bit_cast(uint32_t, h);
+  }
+}
+// Four e4m3 codes in one dword -> four 16-bit values in two dwords.
+template <bool kToBf16>
+__device__ __forceinline__ u32x2 e4m3x4_to(uint32_t w) {
+  return u32x2{e4m3x2_to<kToBf16, false>(w), e4m3x2_to<kToBf16, true>(w)};
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  f16x2 h = {(f16)a, (f16)b};
+  return __builtin_bit_cast(uint32_t, h);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  bf16x2 h = {(bf16)a, (bf16)b};
+  return __builtin_bit_cast(uint32_t, h);
+}
+__device__ __forceinline__ float bf16_lo_to_f32(uint32_t w) { return u2f(w << 16); }
+__device__ __forceinline__ float bf16_hi_to_f32(uint32_t w) { return u2f(w & 0xffff0000u); }
+
+template <bool kBf16>
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (kBf16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, kRsrcWord3);
+}
+
+// Cache policy of the K/V stream: every K/V byte is read exactly once per
+// call, so the loads are marked non-temporal (the gfx950 "nt" bit).
+#ifndef FSK_KV_CACHE_POLICY
+#define FSK_KV_CACHE_POLICY 2
+#endif
+constexpr int kKvAux = FSK_KV_CACHE_POLICY;
+
+// Load `kBytes` (4, 8, 16 or 32) from a buffer resource; bytes past the
+// resource's range read as zero.
+template <int kBytes>
+struct Chunk {
+  uint32_t w[kBytes / 4];
+};
+template <int kBytes, int kAux = 0>
+__device__ __forceinline__ Chunk<kBytes> buf_load(__amdgpu_buffer_rsrc_t r, int off) {
+  Chunk<kBytes> c;
+  if constexpr (kBytes == 4) {
+    c.w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kAux);
+  } else if constexpr (kBytes == 8) {
+    u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kAux);
+    c.w[0] = x[0]; c.w[1] = x[1];
+  } else {
+#pragma unroll
+    for (int i = 0; i < kBytes / 16; ++i) {
+      u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, kAux);
+      c.w[4 * i + 0] = x[0]; c.w[4 * i + 1] = x[1]; c.w[4 * i + 2] = x[2]; c.w[4 * i + 3] = x[3];
+    }
+  }
+  return c;
+}
+
+__device__ __forceinline__ int clampi(int x, int lo, int hi) { return x < lo ? lo : (x > hi ? hi : x); }
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// ---------------------------------------------------------------------------
+// Kernel parameters (passed by value)
+// ---------------------------------------------------------------------------
+struct Params {
+  const uint8_t* q;        // query rows
+  int64_t q_sb, q_sh;      // bytes
+  const uint8_t* k;
+  const uint8_t* v;
+  int64_t k_s0, k_sh, k_st;  // bytes; s0 = page stride (paged) / batch stride (dense)
+  int64_t v_s0, v_sh, v_st;
+  const int32_t* lens;     // varlen: cu_seqlens[B+1]; paged: seq_lens[B]; dense: cache_lens[B]
+  const int32_t* starts;   // dense: start offsets or null
+  const int32_t* block_table;
+  int64_t bt_sb;           // elements
+  int max_blocks, num_pages, page_size;
+  int kv_extent;           // varlen: total rows; dense: S_max
+  const float* q_scale;
+  const float* k_scale;
+  const float* v_scale;
+  float score_scale;       // sm_scale * log2(e)
+  int B, Hkv, G, n_hb;
+  int chunk;               // tokens per unit (multiple of 32)
+  int u_max;               // workspace capacity in units
+  int32_t* plan;           // [B+1] unit prefix offsets
+  float* part_ml;          // [u_max, Hkv, G, 2]
+  float* part_acc;         // [u_max, Hkv, G, D]
+};
+
+// Token range [start, start+len) of sequence b in its layout's row space.
+template <int kLayout>
+__device__ __forceinline__ void seq_range(const Params& p, int b, int& start, int& len) {
+  if constexpr (kLayout == kVarlen) {
+    int s = clampi(p.lens[b], 0, p.kv_extent);
+    int e = clampi(p.lens[b + 1], s, p.kv_extent);
+    start = s;
+    len = e - s;
+  } else if constexpr (kLayout == kPaged) {
+    start = 0;
+    len = clampi(p.lens[b], 0, p.max_blocks * p.page_size);
+  } else {
+    int e = clampi(p.lens[b], 0, p.kv_extent);
+    int s = p.starts ? clampi(p.starts[b], 0, e) : 0;
+    start = s;
+    len = e - s;
+  }
+}
+
+// Base addresses of rows [t, t+16) (sequence-local token t, a multiple of 16)
+// of kv head `kvh`, and how many of those rows are valid.  This is the single
+// page-addressing routine of the library: the decode kernels and the
+// fsk_paged_gather debug entry point both go through it.
+struct HalfTile {
+  const uint8_t* k;
+  const uint8_t* v;
+  int rows;
+};
+template <int kLayout>
+__device__ __forceinline__ HalfTile half_tile(const Params& p, int b, int start, int len, int kvh,
+                                              int t) {
+  HalfTile h;
+  h.rows = clampi(len - t, 0, 16);
+  if constexpr (kLayout == kVarlen) {
+    int64_t row = (int64_t)start + t;
+    if (h.rows == 0) row = 0;
+    h.k = p.k + row * p.k_st + kvh * p.k_sh;
+    h.v = p.v + row * p.v_st + kvh * p.v_sh;
+  } else if constexpr (kLayout == kPaged) {
+    int page = 0, off = 0;
+    if (h.rows > 0) {
+      int lp = t / p.page_size;
+      off = t - lp * p.page_size;
+      page = clampi(p.block_table[(int64_t)b * p.bt_sb + lp], 0, p.num_pages - 1);
+    }
+    h.k = p.k + (int64_t)page * p.k_s0 + kvh * p.k_sh + off * p.k_st;
+    h.v = p.v + (int64_t)page * p.v_s0 + kvh * p.v_sh + off * p.v_st;
+  } else {
+    int64_t row = (int64_t)start + t;
+    if (h.rows == 0) row = 0;
+    h.k = p.k + (int64_t)b * p.k_s0 + kvh * p.k_sh + row * p.k_st;
+    h.v = p.v + (int64_t)b * p.v_s0 + kvh * p.v_sh + row * p.v_st;
+  }
+  return h;
+}
+
+// Builds the unit prefix table in LDS (pre[b] = first unit of sequence b,
+// pre[B] = total units, clamped to the workspace capacity) and returns the
+// total.  Workgroup 0 also publishes it for the reduce kernel.
+template <int kLayout>
+__device__ int build_plan(const Params& p, int32_t* pre) {
+  const int lane = threadIdx.x;
+  int carry = 0;
+  for (int b0 = 0; b0 < p.B; b0 += kWave) {
+    int b = b0 + lane;
+    int n = 0;
+    if (b < p.B) {
+      int start, len;
+      seq_range<kLayout>(p, b, start, len);
+      n = (len + p.chunk - 1) / p.chunk;
+    }
+    int incl = n;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      int y = __shfl_up(incl, off, kWave);
+      if (lane >= off) incl += y;
+    }
+    if (b < p.B) pre[b] = min(carry + incl - n, p.u_max);
+    carry += __shfl(incl, kWave - 1, kWave);
+  }
+  const int total = min(carry, p.u_max);
+  if (lane == 0) pre[p.B] = total;
+  __syncthreads();
+  if (blockIdx.x == 0) {
+    for (int b = lane; b <= p.B; b += kWave) p.plan[b] = pre[b];
+  }
+  return total;
+}
+
+// Largest b with pre[b] <= u (u < pre[B]).
+__device__ __forceinline__ int find_seq(const int32_t* pre, int B, int u) {
+  int lo = 0, hi = B;
+  while (hi - lo > 1) {
+    int mid = (lo + hi) >> 1;
+    if (pre[mid] <= u) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+// ---------------------------------------------------------------------------
+// Partial kernel
+// ---------------------------------------------------------------------------
+// Lane l = 16*g + c (g = k-group 0..3, c = column 0..15).
+//
+// QK (v_mfma_f32_16x16x32, A = K rows, B = Q^T columns): for the 16-token half
+// h2 of a tile and k-step i, lane l holds 8 head_dim values of token row c
+// (A) and of query head c (B); which 8 is fixed by qk_dim0(i, g) for both
+// operands (any consistent split of head_dim over the k-slots gives the same
+// dot product).  Output: lane l holds S^T[token 4g+r][head c], r = 0..3.
+//
+// PV (A = V^T rows, B = P^T columns): k-slot s = 0..7 of k-group g is token
+// tau(g, s) = 16*(s/4) + 4g + (s%4) of the tile, which is exactly where the QK
+// output left P, so P needs no data movement.  MFMA j (0..D/16-1) treats
+// column c as head_dim element (D/16)*c + j; the lane therefore loads the
+// D/16 consecutive elements [(D/16)c, (D/16)(c+1)) of each of its 8 token rows
+// and transposes them in registers with v_perm_b32.  Output: lane l holds
+// O[head c][(D/16)(4g+r) + j].
+//
+// Each wave software-pipelines its unit: the K/V loads of tile n+1 are in
+// flight while tile n is computed.  Paged units read their page ids once, into
+// a 128-entry window (two VGPRs, entry i in lane i % 64), so no block-table
+// load sits in front of a K/V load.
+
+// First head_dim element of k-step i for k-group g (the same for Q and K).
+template <bool kKvFp8>
+__device__ __forceinline__ int qk_dim0(int i, int g) {
+  // 16-bit KV: k-step i reads the 16-byte chunk 4i+g of a row.
+  // e4m3 KV: one 16-byte chunk (4(i/2)+g) covers k-steps i and i+1.
+  return kKvFp8 ? 16 * (4 * (i >> 1) + g) + 8 * (i & 1) : 8 * (4 * i + g);
+}
+
+template <int D, int kKV>
+struct TileRegs {
+  static constexpr bool kFp8 = (kKV == kE4M3);
+  static constexpr int kSteps = D / 32;
+  static constexpr int kKLoads = kFp8 ? kSteps / 2 : kSteps;  // 16-byte K loads per half
+  static constexpr int kVBytes = (D / 16) * (kFp8 ? 1 : 2);   // V bytes per row per lane
+  u32x4 k[2][kKLoads];
+  Chunk<kVBytes> v[8];
+  int nrow[2];  // valid rows of each 16-token half (wave-uniform)
+};
+
+struct Unit {
+  int b, kvh, start, len, t_begin, t_end;
+  int p_first;     // paged: first logical page of the unit
+  int win0, win1;  // paged: physical page of logical page p_first + lane (+64)
+};
+
+template <int kLayout>
+__device__ __forceinline__ HalfTile unit_half(const Params& p, const Unit& un, int t) {
+  HalfTile h;
+  h.rows = uniform(clampi(un.t_end - t, 0, 16));
+  if constexpr (kLayout == kPaged) {
+    int page = 0, off = 0;
+    if (h.rows > 0) {
+      const int lp = t / p.page_size;
+      off = t - lp * p.page_size;
+      const int idx = lp - un.p_first;  // 0 .. 127
+      page = idx < 64 ? __builtin_amdgcn_readlane(un.win0, idx) : __builtin_amdgcn_readlane(un.win1, idx - 64);
+    }
+    h.k = p.k + (int64_t)page * p.k_s0 + un.kvh * p.k_sh + off * p.k_st;
+    h.v = p.v + (int64_t)page * p.v_s0 + un.kvh * p.v_sh + off * p.v_st;
+  } else {
+    HalfTile a = half_tile<kLayout>(p, un.b, un.start, un.len, un.kvh, h.rows > 0 ? t : 0);
+    h.k = a.k;
+    h.v = a.v;
+  }
+  return h;
+}
+
+template <int D, int kKV, int kLayout>
+__device__ __forceinline__ void issue_tile(TileRegs<D, kKV>& T, const Params& p, const Unit& un, int t,
+                                           int g, int c) {
+  using TR = TileRegs<D, kKV>;
+  constexpr int kElem = TR::kFp8 ? 1 : 2;
+  const int kst = (int)p.k_st, vst = (int)p.v_st;
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2) {
+    const HalfTile ht = unit_half<kLayout>(p, un, t + 16 * h2);
+    T.nrow[h2] = ht.rows;
+    const int kbytes = ht.rows > 0 ? (ht.rows - 1) * kst + D * kElem : 0;
+    const int vbytes = ht.rows > 0 ? (ht.rows - 1) * vst + D * kElem : 0;
+    const auto rk = make_rsrc(ht.k, kbytes);
+    const auto rv = make_rsrc(ht.v, vbytes);
+#pragma unroll
+    for (int j = 0; j < TR::kKLoads; ++j) {
+      const Chunk<16> x = buf_load<16, kKvAux>(rk, c * kst + 16 * (4 * j + g));
+      T.k[h2][j] = u32x4{x.w[0], x.w[1], x.w[2], x.w[3]};
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      T.v[4 * h2 + r] = buf_load<TR::kVBytes, kKvAux>(rv, (4 * g + r) * vst + c * TR::kVBytes);
+  }
+}
+
+template <int D, int kQ, int kKV>
+struct Softmax {
+  static constexpr bool kQkBf16 = (kQ == kBF16);   // QK operand type
+  static constexpr bool kPvBf16 = (kKV == kBF16);  // PV operand type (e4m3 V -> f16)
+  static constexpr int kSteps = D / 32;
+  static constexpr int kDpc = D / 16;
+  float m_run, l_run;
+  f32x4 acc[kDpc];
+};
+
+template <int D, int kQ, int kKV>
+__device__ __forceinline__ void compute_tile(const TileRegs<D, kKV>& T, Softmax<D, kQ, kKV>& st,
+                                             const u32x4 (&qop)[D / 32], float sscale, int g) {
+  using TR = TileRegs<D, kKV>;
+  using SM = Softmax<D, kQ, kKV>;
+  constexpr int kSteps = SM::kSteps;
+  constexpr int kDpc = SM::kDpc;
+
+  // ---- S^T = K Q^T
+  f32x4 s[2];
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2) {
+    s[h2] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < kSteps; ++i) {
+      u32x4 kop;
+      if constexpr (TR::kFp8) {
+        const u32x4 raw = T.k[h2][i >> 1];
+        const u32x2 a = e4m3x4_to<SM::kQkBf16>(raw[2 * (i & 1)]);
+        const u32x2 bb = e4m3x4_to<SM::kQkBf16>(raw[2 * (i & 1) + 1]);
+        kop = u32x4{a[0], a[1], bb[0], bb[1]};
+      } else {
+        kop = T.k[h2][i];
+      }
+      s[h2] = mfma16x16x32<SM::kQkBf16>(kop, qop[i], s[h2]);
+    }
+  }
+
+  // ---- online softmax over this tile (log2 domain)
+  float sv[8];
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float x = s[h2][r] * sscale;
+      if (4 * g + r >= T.nrow[h2]) x = -INFINITY;
+      sv[4 * h2 + r] = x;
+    }
+  float mt = sv[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) mt = fmaxf(mt, sv[i]);
+  mt = group4_max(mt);
+  const float m_new = fmaxf(st.m_run, mt);
+  const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+  if (__builtin_amdgcn_ballot_w64(m_new > st.m_run) != 0) {
+    const float alpha = __builtin_amdgcn_exp2f(st.m_run - m_use);
+    st.l_run *= alpha;
+#pragma unroll
+    for (int j = 0; j < kDpc; ++j) st.acc[j] *= alpha;
+  }
+  st.m_run = m_new;
+  float pv[8];
+  float psum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    pv[i] = __builtin_amdgcn_exp2f(sv[i] - m_use);
+    psum += pv[i];
+  }
+  st.l_run += psum;
+
+  // ---- P^T operand(s); bf16 P is split into hi + lo parts
+  u32x4 pop, plo;
+  if constexpr (SM::kPvBf16) {
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      hi[i] = pack_bf16x2(pv[2 * i], pv[2 * i + 1]);
+      lo[i] = pack_bf16x2(pv[2 * i] - bf16_lo_to_f32(hi[i]), pv[2 * i + 1] - bf16_hi_to_f32(hi[i]));
+    }
+    pop = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    plo = u32x4{lo[0], lo[1], lo[2], lo[3]};
+  } else {
+    pop = u32x4{pack_f16x2(pv[0], pv[1]), pack_f16x2(pv[2], pv[3]), pack_f16x2(pv[4], pv[5]),
+                pack_f16x2(pv[6], pv[7])};
+    (void)plo;
+  }
+
+  // ---- V^T operands (16-bit view of each row; e4m3 rows widened to f16)
+  constexpr int kVWords = kDpc / 2;
+  uint32_t vw[8][kVWords];
+#pragma unroll
+  for (int sidx = 0; sidx < 8; ++sidx) {
+    if constexpr (TR::kFp8) {
+#pragma unroll
+      for (int e = 0; e < TR::kVBytes / 4; ++e) {
+        const u32x2 x = e4m3x4_to<false>(T.v[sidx].w[e]);
+        vw[sidx][2 * e] = x[0];
+        vw[sidx][2 * e + 1] = x[1];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < kVWords; ++e) vw[sidx][e] = T.v[sidx].w[e];
+    }
+  }
+  // ---- O^T += V^T P^T
+#pragma unroll
+  for (int j = 0; j < kDpc; ++j) {
+    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+    u32x4 vop;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) vop[m] = __builtin_amdgcn_perm(vw[2 * m + 1][j >> 1], vw[2 * m][j >> 1], sel);
+    st.acc[j] = mfma16x16x32<SM::kPvBf16>(vop, pop, st.acc[j]);
+    if constexpr (SM::kPvBf16) st.acc[j] = mfma16x16x32<true>(vop, plo, st.acc[j]);
+  }
+}
+
+template <int D, int kQ, int kKV, int kLayout>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void partial_kernel(Params p) {
+  using TR = TileRegs<D, kKV>;
+  using SM = Softmax<D, kQ, kKV>;
+  constexpr bool kKvFp8 = TR::kFp8;
+  constexpr int kSteps = SM::kSteps;
+  constexpr int kDpc = SM::kDpc;
+  // Two tiles of registers fit the 2-waves-per-SIMD budget up to D = 128.
+  constexpr bool kPipeline = (D <= 128);
+  static_assert(kKV != kBF16 || kQ == kBF16, "bf16 KV needs bf16 Q");
+  static_assert(kKV != kF16 || kQ != kBF16, "f16 KV needs f16 Q");
+
+  extern __shared__ int32_t s_pre[];
+  const int lane = threadIdx.x;
+  const int g = lane >> 4;
+  const int c = lane & 15;
+
+  const int total_units = build_plan<kLayout>(p, s_pre);
+  const int NH = p.Hkv * p.n_hb;
+  const int64_t W = (int64_t)total_units * NH;
+  const float k_scale = kKvFp8 ? p.k_scale[0] : 1.0f;
+  const float v_scale = kKvFp8 ? p.v_scale[0] : 1.0f;
+  const float sscale = p.score_scale * k_scale;
+
+  for (int64_t w = blockIdx.x; w < W; w += gridDim.x) {
+    const int u = (int)(w / NH);
+    const int hh = (int)(w - (int64_t)u * NH);
+    Unit un;
+    un.kvh = hh / p.n_hb;
+    const int hb = hh - un.kvh * p.n_hb;
+    un.b = uniform(find_seq(s_pre, p.B, u));
+    const int cidx = u - uniform(s_pre[un.b]);
+    seq_range<kLayout>(p, un.b, un.start, un.len);
+    un.start = uniform(un.start);
+    un.len = uniform(un.len);
+    un.t_begin = cidx * p.chunk;
+    un.t_end = min(un.t_begin + p.chunk, un.len);
+    un.p_first = 0;
+    un.win0 = un.win1 = 0;
+    if constexpr (kLayout == kPaged) {
+      un.p_first = un.t_begin / p.page_size;
+      const int npg = (un.t_end - 1) / p.page_size - un.p_first + 1;  // <= 128 (chunk <= 2048)
+      const int32_t* row = p.block_table + (int64_t)un.b * p.bt_sb + un.p_first;
+      if (lane < npg) un.win0 = clampi(row[lane], 0, p.num_pages - 1);
+      if (lane + 64 < npg) un.win1 = clampi(row[lane + 64], 0, p.num_pages - 1);
+    }
+
+    // ---- Q^T operand: head c of this head block, zero for padding heads.
+    const int head = hb * 16 + c;
+    const bool head_ok = head < p.G;
+    u32x4 qop[kSteps];
+    {
+      const uint8_t* qrow =
+          p.q + (int64_t)un.b * p.q_sb + (int64_t)(un.kvh * p.G + (head_ok ? head : 0)) * p.q_sh;
+#pragma unroll
+      for (int i = 0; i < kSteps; ++i) {
+        const int d0 = qk_dim0<kKvFp8>(i, g);
+        u32x4 x = {0, 0, 0, 0};
+        if (head_ok) {
+          if constexpr (kQ == kE4M3) {
+            // q = f16(f32(q8) * scale_q)  (triton_gqa_decode_hf_fp8.py:47-50)
+            const u32x2 raw = *(const u32x2*)(qrow + d0);
+            const float sq = p.q_scale[0];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(raw[e], false);
+              const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(raw[e], true);
+              x[2 * e] = pack_f16x2(lo[0] * sq, lo[1] * sq);
+              x[2 * e + 1] = pack_f16x2(hi[0] * sq, hi[1] * sq);
+            }
+          } else {
+            x = *(const u32x4*)(qrow + 2 * d0);
+          }
+        }
+        qop[i] = x;
+      }
+    }
+
+    SM st;
+    st.m_run = -INFINITY;
+    st.l_run = 0.f;
+#pragma unroll
+    for (int j = 0; j < kDpc; ++j) st.acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    if constexpr (kPipeline) {
+      TR ta, tb;
+      int t = un.t_begin;
+      issue_tile<D, kKV, kLayout>(ta, p, un, t, g, c);
+      while (true) {
+        if (t + 32 < un.t_end) issue_tile<D, kKV, kLayout>(tb, p, un, t + 32, g, c);
+        compute_tile<D, kQ, kKV>(ta, st, qop, sscale, g);
+        t += 32;
+        if (t >= un.t_end) break;
+        if (t + 32 < un.t_end) issue_tile<D, kKV, kLayout>(ta, p, un, t + 32, g, c);
+        compute_tile<D, kQ, kKV>(tb, st, qop, sscale, g);
+        t += 32;
+        if (t >= un.t_end) break;
+      }
+    } else {
+      TR ta;
+      for (int t = un.t_begin; t < un.t_end; t += 32) {
+        issue_tile<D, kKV, kLayout>(ta, p, un, t, g, c);
+        compute_tile<D, kQ, kKV>(ta, st, qop, sscale, g);
+      }
+    }
+
+    // ---- unit epilogue: fp32 partial for each real head of the block
+    const float l_tot = group4_sum(st.l_run);
+    if (head_ok) {
+      const int64_t idx = ((int64_t)u * p.Hkv + un.kvh) * p.G + head;
+      float* dst = p.part_acc + idx * D + kDpc * 4 * g;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < kDpc; j += 4) {
+          const f32x4 o = {st.acc[j][r] * v_scale, st.acc[j + 1][r] * v_scale, st.acc[j + 2][r] * v_scale,
+                           st.acc[j + 3][r] * v_scale};
+          *(f32x4*)(dst + kDpc * r + j) = o;
+        }
+      if (g == 0) *(f32x2*)(p.part_ml + 2 * idx) = f32x2{st.m_run, l_tot};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Reduce kernel: LSE merge of a sequence's partials + sink fold.
+// ---------------------------------------------------------------------------
+struct ReduceParams {
+  const int32_t* plan;
+  const float* part_ml;
+  const float* part_acc;
+  const float* s_aux;
+  int sink_mode;
+  uint8_t* out;
+  int64_t o_sb, o_sh;  // bytes
+  int Hq, Hkv, G;
+};
+
+constexpr int kReduceWaves = 4;
+
+template <int D, int kOut>
+__global__ __launch_bounds__(64 * kReduceWaves) void reduce_kernel(ReduceParams p) {
+  // One workgroup per (query head, sequence); wave w merges units
+  // u0 + w, u0 + w + 4, ... and the waves combine through LDS.
+  constexpr int kE = D / kWave;  // output elements per lane
+  __shared__ float s_red[kReduceWaves];
+  __shared__ float s_num[kReduceWaves][D];
+  __shared__ float s_den[kReduceWaves];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wv = tid / kWave;
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int kvh = h / p.G;
+  const int hg = h - kvh * p.G;
+  const int u0 = p.plan[b];
+  const int n = p.plan[b + 1] - u0;
+  const int64_t base = ((int64_t)u0 * p.Hkv + kvh) * p.G + hg;  // partial index of unit u0
+  const int64_t ustride = (int64_t)p.Hkv * p.G;                 // between consecutive units
+
+  float M = -INFINITY;
+  for (int i = tid; i < n; i += kWave * kReduceWaves) M = fmaxf(M, p.part_ml[2 * (base + i * ustride)]);
+  M = wave_max(M);
+  if (lane == 0) s_red[wv] = M;
+  __syncthreads();
+  M = s_red[0];
+#pragma unroll
+  for (int w = 1; w < kReduceWaves; ++w) M = fmaxf(M, s_red[w]);
+  const float M_use = (M == -INFINITY) ? 0.f : M;
+
+  float den = 0.f;
+  float num[kE];
+#pragma unroll
+  for (int e = 0; e < kE; ++e) num[e] = 0.f;
+#pragma unroll 4
+  for (int i = wv; i < n; i += kReduceWaves) {
+    const int64_t idx = base + i * ustride;
+    const f32x2 ml = *(const f32x2*)(p.part_ml + 2 * idx);
+    const float* a = p.part_acc + idx * D + lane * kE;
+    float x[kE];
+    if constexpr (kE == 4) {
+      const f32x4 v = *(const f32x4*)a;
+      x[0] = v[0]; x[1] = v[1]; x[2] = v[2]; x[3] = v[3];
+    } else if constexpr (kE == 2) {
+      const f32x2 v = *(const f32x2*)a;
+      x[0] = v[0]; x[1] = v[1];
+    } else {
+      x[0] = a[0];
+    }
+    const float wgt = __builtin_amdgcn_exp2f(ml[0] - M_use);
+    den += ml[1] * wgt;
+#pragma unroll
+    for (int e = 0; e < kE; ++e) num[e] += x[e] * wgt;
+  }
+#pragma unroll
+  for (int e = 0; e < kE; ++e) s_num[wv][lane * kE + e] = num[e];
+  if (lane == 0) s_den[wv] = den;
+  __syncthreads();
+  if (wv != 0) return;
+#pragma unroll
+  for (int w = 1; w < kReduceWaves; ++w) {
+    den += s_den[w];
+#pragma unroll
+    for (int e = 0; e < kE; ++e) num[e] += s_num[w][lane * kE + e];
+  }
+
+  if (p.s_aux) {
+    const float z = p.s_aux[h];
+    if (p.sink_mode == FSK_SINK_EXP) {
+      // Extra logit z with a zero value vector (log2 domain: z * log2 e).
+      const float z2 = z * kLog2e;
+      const float Mn = fmaxf(M, z2);
+      const float Mn_use = (Mn == -INFINITY) ? 0.f : Mn;
+      const float f = __builtin_amdgcn_exp2f(M_use - Mn_use);
+      den = den * f + __builtin_amdgcn_exp2f(z2 - Mn_use);
+#pragma unroll
+      for (int e = 0; e < kE; ++e) num[e] *= f;
+    } else {
+      den += z;  // linear fold relative to the running max (flash_decode_cuda.cu:151-153)
+    }
+  }
+
+  uint8_t* o = p.out + (int64_t)b * p.o_sb + (int64_t)h * p.o_sh;
+#pragma unroll
+  for (int e = 0; e < kE; ++e) {
+    const float val = num[e] / den;
+    const int d = lane * kE + e;
+    if constexpr (kOut == kF32) ((float*)o)[d] = val;
+    else if constexpr (kOut == kF16) ((f16*)o)[d] = (f16)val;
+    else ((bf16*)o)[d] = (bf16)val;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Debug kernels
+// ---------------------------------------------------------------------------
+template <int D, int kElem>
+__global__ __launch_bounds__(64) void paged_gather_kernel(Params p, uint8_t* out, int64_t o_rows) {
+  // grid: (tiles of 16 rows, Hkv, B); out [B, Hkv, o_rows, D] contiguous
+  constexpr int kRowBytes = D * kElem;
+  constexpr int kChunks = kRowBytes / 16;
+  const int t = blockIdx.x * 16;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  int start, len;
+  seq_range<kPaged>(p, b, start, len);
+  HalfTile ht = half_tile<kPaged>(p, b, start, len, kvh, t);
+  const int bytes = ht.rows > 0 ? (ht.rows - 1) * (int)p.k_st + kRowBytes : 0;
+  auto rk = make_rsrc(ht.k, bytes);
+  uint8_t* dst = out + (((int64_t)b * p.Hkv + kvh) * o_rows + t) * kRowBytes;
+  for (int i = threadIdx.x; i < 16 * kChunks; i += kWave) {
+    const int r = i / kChunks, ch = i - r * kChunks;
+    Chunk<16> x = buf_load<16>(rk, r * (int)p.k_st + 16 * ch);
+    *(u32x4*)(dst + r * kRowBytes + 16 * ch) = u32x4{x.w[0], x.w[1], x.w[2], x.w[3]};
+  }
+}
+
+__global__ __launch_bounds__(64) void fp8_table_kernel(uint32_t* out) {
+  // Codes 4l .. 4l+3 through both widening routes.  The raw 16-bit results are
+  // stored as produced (the host widens them to fp32), so the table exercises
+  // exactly the instruction sequence the decode kernels use.
+  const int l = threadIdx.x;
+  const uint32_t w = (uint32_t)(4 * l) | ((uint32_t)(4 * l + 1) << 8) | ((uint32_t)(4 * l + 2) << 16) |
+                     ((uint32_t)(4 * l + 3) << 24);
+  const u32x2 h = e4m3x4_to<false>(w);
+  const u32x2 bb = e4m3x4_to<true>(w);
+  *(u32x2*)(out + 2 * l) = h;
+  *(u32x2*)(out + 128 + 2 * l) = bb;
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+struct Options {
+  int chunk_tokens = 0;  // 0: automatic
+  int waves_per_cu = 8;
+} g_opt;
+
+// Event triples recorded around decode calls while kernel timing is enabled.
+struct Timing {
+  bool enabled = false;
+  std::vector<hipEvent_t> ev;  // 3 per call
+  std::vector<hipEvent_t> spare;
+} g_timing;
+
+hipEvent_t timing_event() {
+  hipEvent_t e = nullptr;
+  if (!g_timing.spare.empty()) {
+    e = g_timing.spare.back();
+    g_timing.spare.pop_back();
+  } else if (hipEventCreate(&e) != hipSuccess) {
+    e = nullptr;
+  }
+  return e;
+}
+
+void timing_mark(hipStream_t s) {
+  if (!g_timing.enabled) return;
+  hipEvent_t e = timing_event();
+  if (e && hipEventRecord(e, s) == hipSuccess) g_timing.ev.push_back(e);
+  else g_timing.enabled = false;  // could not record: stop timing rather than mis-pair
+}
+
+void timing_clear() {
+  for (hipEvent_t e : g_timing.ev) g_timing.spare.push_back(e);
+  g_timing.ev.clear();
+}
+
+int elem_bytes(int dt) {
+  switch (dt) {
+    case FSK_F16: case FSK_BF16: return 2;
+    case FSK_F32: return 4;
+    case FSK_E4M3: return 1;
+    default: return 0;
+  }
+}
+
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+// Split size: aim for about 8 units per CU-wave slot of work, clamped.
+int pick_chunk(int layout, int B, int Hkv, int n_hb, int64_t kv_extent, int page_size, int cus) {
+  if (g_opt.chunk_tokens > 0) return g_opt.chunk_tokens;
+  int64_t est_len;
+  if (layout == FSK_LAYOUT_VARLEN) est_len = cdiv(kv_extent, B);
+  else if (layout == FSK_LAYOUT_PAGED) est_len = kv_extent * page_size;
+  else est_len = kv_extent;
+  const int64_t rows = (int64_t)B * Hkv * n_hb * est_len;
+  int64_t ch = rows / ((int64_t)cus * g_opt.waves_per_cu);
+  ch = (ch + 31) / 32 * 32;
+  if (ch < 128) ch = 128;
+  if (ch > 2048) ch = 2048;
+  return (int)ch;
+}
+
+int64_t unit_bound(int layout, int B, int64_t kv_extent, int page_size, int chunk) {
+  if (layout == FSK_LAYOUT_VARLEN) return cdiv(kv_extent, chunk) + B;
+  if (layout == FSK_LAYOUT_PAGED) return (int64_t)B * cdiv(kv_extent * page_size, chunk);
+  return (int64_t)B * cdiv(kv_extent, chunk);
+}
+
+struct WsLayout {
+  int64_t plan_off, ml_off, acc_off, total;
+};
+WsLayout ws_layout(int B, int Hkv, int G, int D, int64_t u_max) {
+  WsLayout w;
+  w.plan_off = 0;
+  w.ml_off = align256(4 * (int64_t)(B + 1));
+  w.acc_off = w.ml_off + align256(u_max * Hkv * G * 2 * 4);
+  w.total = w.acc_off + align256(u_max * Hkv * G * (int64_t)D * 4);
+  return w;
+}
+
+struct Common {
+  int layout;
+  const void* q; int64_t q_sb, q_sh;
+  const void* k; int64_t k_s0, k_sh, k_st;
+  const void* v; int64_t v_s0, v_sh, v_st;
+  const int32_t* lens; const int32_t* starts;
+  const int32_t* bt; int64_t bt_sb; int max_blocks, num_pages, page_size;
+  int64_t kv_extent;
+  const float* s_aux; int sink_mode;
+  const float *q_scale, *k_scale, *v_scale;
+  void* out; int64_t o_sb, o_sh;
+  int B, Hq, Hkv, D, q_dt, kv_dt, o_dt;
+  float sm_scale;
+  void* ws; int64_t ws_bytes; int chunk;
+  hipStream_t stream;
+};
+
+bool aligned(const void* p, int a) { return ((uintptr_t)p % a) == 0; }
+
+int validate(const Common& c) {
+  if (c.B < 0 || c.Hq <= 0 || c.Hkv <= 0) return fail(FSK_ERR_INVALID, "batch/heads must be positive");
+  if (c.Hq % c.Hkv != 0) return fail(FSK_ERR_INVALID, "num_q_heads must be a multiple of num_kv_heads");
+  if (c.D != 64 && c.D != 128 && c.D != 256) return fail(FSK_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256");
+  if (!c.q || !c.k || !c.v || !c.lens || !c.out) return fail(FSK_ERR_INVALID, "null tensor pointer");
+  if (c.sink_mode != FSK_SINK_EXP && c.sink_mode != FSK_SINK_LINEAR) return fail(FSK_ERR_INVALID, "bad sink_mode");
+  if (c.o_dt != FSK_F16 && c.o_dt != FSK_BF16 && c.o_dt != FSK_F32) return fail(FSK_ERR_UNSUPPORTED, "out dtype must be f16, bf16 or f32");
+  if (c.kv_dt == FSK_E4M3) {
+    if (c.q_dt != FSK_F16 && c.q_dt != FSK_BF16 && !(c.q_dt == FSK_E4M3 && c.layout == FSK_LAYOUT_DENSE))
+      return fail(FSK_ERR_UNSUPPORTED, "e4m3 KV needs f16/bf16 q (e4m3 q only on the dense layout)");
+    if (!c.k_scale || !c.v_scale) return fail(FSK_ERR_INVALID, "e4m3 KV needs k_scale and v_scale");
+  } else if (c.kv_dt == FSK_F16 || c.kv_dt == FSK_BF16) {
+    if (c.q_dt != c.kv_dt) return fail(FSK_ERR_UNSUPPORTED, "q and f16/bf16 KV must share a dtype");
+  } else {
+    return fail(FSK_ERR_UNSUPPORTED, "KV dtype must be f16, bf16 or e4m3");
+  }
+  if (c.q_dt == FSK_E4M3 && !c.q_scale) return fail(FSK_ERR_INVALID, "e4m3 q needs q_scale");
+  if (!(c.sm_scale == c.sm_scale) || !std::isfinite(c.sm_scale)) return fail(FSK_ERR_INVALID, "sm_scale must be finite");
+  const int qe = elem_bytes(c.q_dt), ke = elem_bytes(c.kv_dt), oe = elem_bytes(c.o_dt);
+  // Row starts must be 16-byte aligned (8 for e4m3 q) for the vector loads.
+  const int qa = (c.q_dt == FSK_E4M3) ? 8 : 16;
+  if (!aligned(c.q, qa) || (c.q_sb * qe) % qa || (c.q_sh * qe) % qa) return fail(FSK_ERR_INVALID, "q rows must be 16-byte aligned");
+  if (!aligned(c.k, 16) || !aligned(c.v, 16) || (c.k_st * ke) % 16 || (c.v_st * ke) % 16 || (c.k_sh * ke) % 16 ||
+      (c.v_sh * ke) % 16 || (c.k_s0 * ke) % 16 || (c.v_s0 * ke) % 16)
+    return fail(FSK_ERR_INVALID, "k/v rows must be 16-byte aligned");
+  if (c.k_st < c.D || c.v_st < c.D) return fail(FSK_ERR_INVALID, "k/v token stride must be >= head_dim");
+  if (c.q_sb < 0 || c.q_sh < 0 || c.k_s0 < 0 || c.k_sh < 0 || c.v_s0 < 0 || c.v_sh < 0 || c.o_sb < 0 || c.o_sh < 0)
+    return fail(FSK_ERR_INVALID, "negative stride");
+  if ((c.k_st * ke) * 16 >= (int64_t)1 << 31 || (c.v_st * ke) * 16 >= (int64_t)1 << 31)
+    return fail(FSK_ERR_UNSUPPORTED, "k/v token stride too large");
+  if (!aligned(c.out, 4 * oe) || (c.o_sb * oe) % (4 * oe) || (c.o_sh * oe) % (4 * oe))
+    return fail(FSK_ERR_INVALID, "out rows must be aligned to 4 elements");
+  if (c.kv_extent < 0 || c.kv_extent >= ((int64_t)1 << 31)) return fail(FSK_ERR_UNSUPPORTED, "kv extent out of int32 range");
+  if (c.layout == FSK_LAYOUT_PAGED) {
+    if (!c.bt) return fail(FSK_ERR_INVALID, "null block_table");
+    if (c.page_size <= 0 || c.page_size % 16) return fail(FSK_ERR_UNSUPPORTED, "page_size must be a positive multiple of 16");
+    if (c.num_pages <= 0) return fail(FSK_ERR_INVALID, "num_pages must be positive");
+    if (c.max_blocks < 0 || c.bt_sb < c.max_blocks) return fail(FSK_ERR_INVALID, "bad block_table shape");
+    if ((int64_t)c.max_blocks * c.page_size >= ((int64_t)1 << 31)) return fail(FSK_ERR_UNSUPPORTED, "block table too wide");
+  }
+  if (c.B > 16384) return fail(FSK_ERR_UNSUPPORTED, "batch above 16384");
+  return FSK_OK;
+}
+
+template <int D, int kQ, int kKV, int kLayout>
+void launch_partial(const Params& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((partial_kernel<D, kQ, kKV, kLayout>), dim3(grid), dim3(64), 4 * (p.B + 1), s, p);
+}
+
+template <int D, int kLayout>
+int dispatch_qkv(const Params& p, int grid, int q_dt, int kv_dt, hipStream_t s) {
+  if (kv_dt == FSK_F16) launch_partial<D, kF16, kF16, kLayout>(p, grid, s);
+  else if (kv_dt == FSK_BF16) launch_partial<D, kBF16, kBF16, kLayout>(p, grid, s);
+  else if (q_dt == FSK_F16) launch_partial<D, kF16, kE4M3, kLayout>(p, grid, s);
+  else if (q_dt == FSK_BF16) launch_partial<D, kBF16, kE4M3, kLayout>(p, grid, s);
+  else if constexpr (kLayout == kDense) launch_partial<D, kE4M3, kE4M3, kLayout>(p, grid, s);
+  else return fail(FSK_ERR_UNSUPPORTED, "e4m3 q only on the dense layout");
+  return FSK_OK;
+}
+
+template <int D>
+int dispatch_layout(int layout, const Params& p, int grid, int q_dt, int kv_dt, hipStream_t s) {
+  if (layout == FSK_LAYOUT_VARLEN) return dispatch_qkv<D, kVarlen>(p, grid, q_dt, kv_dt, s);
+  if (layout == FSK_LAYOUT_PAGED) return dispatch_qkv<D, kPaged>(p, grid, q_dt, kv_dt, s);
+  return dispatch_qkv<D, kDense>(p, grid, q_dt, kv_dt, s);
+}
+
+template <int D>
+void launch_reduce(const ReduceParams& rp, int B, int o_dt, hipStream_t s) {
+  dim3 grid(rp.Hq, B);
+  dim3 block(64 * kReduceWaves);
+  if (o_dt == FSK_F16) hipLaunchKernelGGL((reduce_kernel<D, kF16>), grid, block, 0, s, rp);
+  else if (o_dt == FSK_BF16) hipLaunchKernelGGL((reduce_kernel<D, kBF16>), grid, block, 0, s, rp);
+  else hipLaunchKernelGGL((reduce_kernel<D, kF32>), grid, block, 0, s, rp);
+}
+
+int run_decode(const Common& c) {
+  int st = validate(c);
+  if (st != FSK_OK) return st;
+  if (c.B == 0) return FSK_OK;
+  const int G = c.Hq / c.Hkv;
+  const int n_hb = (G + 15) / 16;
+  const int cus = device_cus();
+  int chunk = c.chunk > 0 ? c.chunk : pick_chunk(c.layout, c.B, c.Hkv, n_hb, c.kv_extent, c.page_size, cus);
+  if (chunk % 32 != 0 || chunk <= 0) return fail(FSK_ERR_INVALID, "chunk_tokens must be a positive multiple of 32");
+  if (c.layout == FSK_LAYOUT_PAGED && chunk > 2048)
+    return fail(FSK_ERR_UNSUPPORTED, "paged decode takes chunk_tokens <= 2048");
+  const int64_t u_max = unit_bound(c.layout, c.B, c.kv_extent, c.page_size, chunk);
+  if (u_max >= ((int64_t)1 << 31) / (c.Hkv * (int64_t)n_hb)) return fail(FSK_ERR_UNSUPPORTED, "too many work units");
+  const WsLayout wl = ws_layout(c.B, c.Hkv, G, c.D, u_max);
+  if (!c.ws || c.ws_bytes < wl.total || !aligned(c.ws, 256))
+    return fail(FSK_ERR_WORKSPACE, "workspace missing, unaligned or smaller than fsk_workspace_bytes()");
+
+  const int qe = elem_bytes(c.q_dt), ke = elem_bytes(c.kv_dt), oe = elem_bytes(c.o_dt);
+  Params p;
+  memset(&p, 0, sizeof(p));
+  p.q = (const uint8_t*)c.q;
+  p.q_sb = c.q_sb * qe; p.q_sh = c.q_sh * qe;
+  p.k = (const uint8_t*)c.k; p.v = (const uint8_t*)c.v;
+  p.k_s0 = c.k_s0 * ke; p.k_sh = c.k_sh * ke; p.k_st = c.k_st * ke;
+  p.v_s0 = c.v_s0 * ke; p.v_sh = c.v_sh * ke; p.v_st = c.v_st * ke;
+  p.lens = c.lens; p.starts = c.starts;
+  p.block_table = c.bt; p.bt_sb = c.bt_sb; p.max_blocks = c.max_blocks;
+  p.num_pages = c.num_pages; p.page_size = c.page_size > 0 ? c.page_size : 16;
+  p.kv_extent = (int)c.kv_extent;
+  p.q_scale = c.q_scale; p.k_scale = c.k_scale; p.v_scale = c.v_scale;
+  p.score_scale = c.sm_scale * kLog2e;
+  p.B = c.B; p.Hkv = c.Hkv; p.G = G; p.n_hb = n_hb;
+  p.chunk = chunk; p.u_max = (int)u_max;
+  uint8_t* ws = (uint8_t*)c.ws;
+  p.plan = (int32_t*)(ws + wl.plan_off);
+  p.part_ml = (float*)(ws + wl.ml_off);
+  p.part_acc = (float*)(ws + wl.acc_off);
+
+  const int64_t w_max = u_max * c.Hkv * n_hb;
+  const int64_t grid64 = std::min<int64_t>(w_max, (int64_t)cus * g_opt.waves_per_cu);
+  const int grid = (int)std::max<int64_t>(grid64, 1);
+
+  (void)hipGetLastError();
+  timing_mark(c.stream);
+  int rc;
+  if (c.D == 64) rc = dispatch_layout<64>(c.layout, p, grid, c.q_dt, c.kv_dt, c.stream);
+  else if (c.D == 128) rc = dispatch_layout<128>(c.layout, p, grid, c.q_dt, c.kv_dt, c.stream);
+  else rc = dispatch_layout<256>(c.layout, p, grid, c.q_dt, c.kv_dt, c.stream);
+  if (rc != FSK_OK) {
+    if (g_timing.enabled && !g_timing.ev.empty()) {  // drop this call's first mark
+      g_timing.spare.push_back(g_timing.ev.back());
+      g_timing.ev.pop_back();
+    }
+    return rc;
+  }
+
+  timing_mark(c.stream);
+  ReduceParams rp;
+  rp.plan = p.plan; rp.part_ml = p.part_ml; rp.part_acc = p.part_acc;
+  rp.s_aux = c.s_aux; rp.sink_mode = c.sink_mode;
+  rp.out = (uint8_t*)c.out; rp.o_sb = c.o_sb * oe; rp.o_sh = c.o_sh * oe;
+  rp.Hq = c.Hq; rp.Hkv = c.Hkv; rp.G = G;
+  if (c.D == 64) launch_reduce<64>(rp, c.B, c.o_dt, c.stream);
+  else if (c.D == 128) launch_reduce<128>(rp, c.B, c.o_dt, c.stream);
+  else launch_reduce<256>(rp, c.B, c.o_dt, c.stream);
+  timing_mark(c.stream);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(FSK_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(e));
+  return FSK_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+const char* fsk_last_error(void) { return g_err.c_str(); }
+
+int fsk_version(void) { return 1; }
+
+int fsk_set_option(const char* name, int64_t value) {
+  if (!name) return fail(FSK_ERR_INVALID, "null option name");
+  if (!strcmp(name, "chunk_tokens")) {
+    if (value < 0 || value % 32 || value > (1 << 20)) return fail(FSK_ERR_INVALID, "chunk_tokens: 0 or a multiple of 32");
+    g_opt.chunk_tokens = (int)value;
+    return FSK_OK;
+  }
+  if (!strcmp(name, "waves_per_cu")) {
+    if (value < 1 || value > 64) return fail(FSK_ERR_INVALID, "waves_per_cu in [1, 64]");
+    g_opt.waves_per_cu = (int)value;
+    return FSK_OK;
+  }
+  return fail(FSK_ERR_INVALID, std::string("unknown option ") + name);
+}
+
+int fsk_enable_kernel_timing(int enable) {
+  timing_clear();
+  g_timing.enabled = enable != 0;
+  return FSK_OK;
+}
+
+int fsk_kernel_timing(double* partial_ms, double* total_ms, int64_t* calls) {
+  if (!partial_ms || !total_ms || !calls) return fail(FSK_ERR_INVALID, "null pointer");
+  *partial_ms = *total_ms = 0.0;
+  *calls = 0;
+  const size_t n = g_timing.ev.size() / 3 * 3;
+  if (n) {
+    hipError_t e = hipEventSynchronize(g_timing.ev[n - 1]);
+    if (e != hipSuccess) {
+      timing_clear();
+      return fail(FSK_ERR_HIP, std::string("hipEventSynchronize: ") + hipGetErrorString(e));
+    }
+  }
+  for (size_t i = 0; i < n; i += 3) {
+    float a = 0.f, b = 0.f;
+    if (hipEventElapsedTime(&a, g_timing.ev[i], g_timing.ev[i + 1]) != hipSuccess ||
+        hipEventElapsedTime(&b, g_timing.ev[i], g_timing.ev[i + 2]) != hipSuccess) {
+      timing_clear();
+      return fail(FSK_ERR_HIP, "hipEventElapsedTime failed");
+    }
+    *partial_ms += a;
+    *total_ms += b;
+    *calls += 1;
+  }
+  timing_clear();
+  return FSK_OK;
+}
+
+int64_t fsk_workspace_bytes(int layout, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                            int64_t kv_extent, int page_size, int chunk_tokens) {
+  if (layout < 0 || layout > 2) return fail(FSK_ERR_INVALID, "bad layout");
+  if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads || kv_extent < 0)
+    return fail(FSK_ERR_INVALID, "bad shape");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return fail(FSK_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256");
+  if (layout == FSK_LAYOUT_PAGED && (page_size <= 0 || page_size % 16)) return fail(FSK_ERR_UNSUPPORTED, "page_size must be a positive multiple of 16");
+  if (chunk_tokens < 0 || chunk_tokens % 32) return fail(FSK_ERR_INVALID, "chunk_tokens: 0 or a multiple of 32");
+  const int G = num_q_heads / num_kv_heads;
+  const int n_hb = (G + 15) / 16;
+  const int B = batch > 0 ? batch : 1;
+  const int chunk = chunk_tokens > 0 ? chunk_tokens
+                                      : pick_chunk(layout, B, num_kv_heads, n_hb, kv_extent, page_size, device_cus());
+  const int64_t u_max = unit_bound(layout, B, kv_extent, page_size, chunk);
+  return ws_layout(B, num_kv_heads, G, head_dim, u_max).total;
+}
+
+int fsk_decode_varlen(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k, int64_t k_stride_t,
+                      int64_t k_stride_h, const void* v, int64_t v_stride_t, int64_t v_stride_h,
+                      const int32_t* cu_seqlens, int64_t total_tokens, const float* s_aux, int sink_mode,
+                      const float* k_scale, const float* v_scale, void* out, int64_t o_stride_b,
+                      int64_t o_stride_h, int batch, int num_q_heads, int num_kv_heads, int head_dim, int q_dtype,
+                      int kv_dtype, int out_dtype, float sm_scale, void* workspace, int64_t workspace_bytes,
+                      int chunk_tokens, void* stream) {
+  Common c;
+  memset(&c, 0, sizeof(c));
+  c.layout = FSK_LAYOUT_VARLEN;
+  c.q = q; c.q_sb = q_stride_b; c.q_sh = q_stride_h;
+  c.k = k; c.k_st = k_stride_t; c.k_sh = k_stride_h;
+  c.v = v; c.v_st = v_stride_t; c.v_sh = v_stride_h;
+  c.lens = cu_seqlens; c.kv_extent = total_tokens;
+  c.s_aux = s_aux; c.sink_mode = sink_mode; c.k_scale = k_scale; c.v_scale = v_scale;
+  c.out = out; c.o_sb = o_stride_b; c.o_sh = o_stride_h;
+  c.B = batch; c.Hq = num_q_heads; c.Hkv = num_kv_heads; c.D = head_dim;
+  c.q_dt = q_dtype; c.kv_dt = kv_dtype; c.o_dt = out_dtype; c.sm_scale = sm_scale;
+  c.ws = workspace; c.ws_bytes = workspace_bytes; c.chunk = chunk_tokens; c.stream = (hipStream_t)stream;
+  return run_decode(c);
+}
+
+int fsk_decode_paged(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_pool, int64_t k_stride_p,
+                     int64_t k_stride_h, int64_t k_stride_t, const void* v_pool, int64_t v_stride_p,
+                     int64_t v_stride_h, int64_t v_stride_t, const int32_t* block_table, int64_t bt_stride_b,
+                     int max_blocks, const int32_t* seq_lens, int num_pages, int page_size, const float* s_aux,
+                     int sink_mode, const float* k_scale, const float* v_scale, void* out, int64_t o_stride_b,
+                     int64_t o_stride_h, int batch, int num_q_heads, int num_kv_heads, int head_dim, int q_dtype,
+                     int kv_dtype, int out_dtype, float sm_scale, void* workspace, int64_t workspace_bytes,
+                     int chunk_tokens, void* stream) {
+  Common c;
+  memset(&c, 0, sizeof(c));
+  c.layout = FSK_LAYOUT_PAGED;
+  c.q = q; c.q_sb = q_stride_b; c.q_sh = q_stride_h;
+  c.k = k_pool; c.k_s0 = k_stride_p; c.k_sh = k_stride_h; c.k_st = k_stride_t;
+  c.v = v_pool; c.v_s0 = v_stride_p; c.v_sh = v_stride_h; c.v_st = v_stride_t;
+  c.bt = block_table; c.bt_sb = bt_stride_b; c.max_blocks = max_blocks;
+  c.lens = seq_lens; c.num_pages = num_pages; c.page_size = page_size; c.kv_extent = max_blocks;
+  c.s_aux = s_aux; c.sink_mode = sink_mode; c.k_scale = k_scale; c.v_scale = v_scale;
+  c.out = out; c.o_sb = o_stride_b; c.o_sh = o_stride_h;
+  c.B = batch; c.Hq = num_q_heads; c.Hkv = num_kv_heads; c.D = head_dim;
+  c.q_dt = q_dtype; c.kv_dt = kv_dtype; c.o_dt = out_dtype; c.sm_scale = sm_scale;
+  c.ws = workspace; c.ws_bytes = workspace_bytes; c.chunk = chunk_tokens; c.stream = (hipStream_t)stream;
+  return run_decode(c);
+}
+
+int fsk_decode_dense(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k, int64_t k_stride_b,
+                     int64_t k_stride_h, int64_t k_stride_t, const void* v, int64_t v_stride_b, int64_t v_stride_h,
+                     int64_t v_stride_t, int64_t max_seqlen, const int32_t* cache_lens,
+                     const int32_t* start_offsets, const float* s_aux, int sink_mode, const float* q_scale,
+                     const float* k_scale, const float* v_scale, void* out, int64_t o_stride_b,
+                     int64_t o_stride_h, int batch, int num_q_heads, int num_kv_heads, int head_dim, int q_dtype,
+                     int kv_dtype, int out_dtype, float sm_scale, void* workspace, int64_t workspace_bytes,
+                     int chunk_tokens, void* stream) {
+  Common c;
+  memset(&c, 0, sizeof(c));
+  c.layout = FSK_LAYOUT_DENSE;
+  c.q = q; c.q_sb = q_stride_b; c.q_sh = q_stride_h;
+  c.k = k; c.k_s0 = k_stride_b; c.k_sh = k_stride_h; c.k_st = k_stride_t;
+  c.v = v; c.v_s0 = v_stride_b; c.v_sh = v_stride_h; c.v_st = v_stride_t;
+  c.kv_extent = max_seqlen; c.lens = cache_lens; c.starts = start_offsets;
+  c.s_aux = s_aux; c.sink_mode = sink_mode; c.q_scale = q_scale; c.k_scale = k_scale; c.v_scale = v_scale;
+  c.out = out; c.o_sb = o_stride_b; c.o_sh = o_stride_h;
+  c.B = batch; c.Hq = num_q_heads; c.Hkv = num_kv_heads; c.D = head_dim;
+  c.q_dt = q_dtype; c.kv_dt = kv_dtype; c.o_dt = out_dtype; c.sm_scale = sm_scale;
+  c.ws = workspace; c.ws_bytes = workspace_bytes; c.chunk = chunk_tokens; c.stream = (hipStream_t)stream;
+  return run_decode(c);
+}
+
+int fsk_paged_gather(const void* pool, int64_t stride_p, int64_t stride_h, int64_t stride_t,
+                     const int32_t* block_table, int64_t bt_stride_b, int max_blocks, const int32_t* seq_lens,
+                     int num_pages, int page_size, int batch, int num_kv_heads, int head_dim, int dtype, void* out,
+                     void* stream) {
+  if (!pool || !block_table || !seq_lens || !out) return fail(FSK_ERR_INVALID, "null pointer");
+  if (batch < 0 || num_kv_heads <= 0 || max_blocks < 0 || num_pages <= 0 || bt_stride_b < max_blocks)
+    return fail(FSK_ERR_INVALID, "bad shape");
+  if (page_size <= 0 || page_size % 16) return fail(FSK_ERR_UNSUPPORTED, "page_size must be a positive multiple of 16");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return fail(FSK_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256");
+  const int e = elem_bytes(dtype);
+  if (e != 1 && e != 2) return fail(FSK_ERR_UNSUPPORTED, "dtype must be f16, bf16 or e4m3");
+  if (!aligned(pool, 16) || !aligned(out, 16) || (stride_p * e) % 16 || (stride_h * e) % 16 || (stride_t * e) % 16 ||
+      stride_t < head_dim)
+    return fail(FSK_ERR_INVALID, "pool rows must be 16-byte aligned and non-overlapping");
+  if ((int64_t)max_blocks * page_size >= ((int64_t)1 << 31)) return fail(FSK_ERR_UNSUPPORTED, "block table too wide");
+  if (batch == 0 || max_blocks == 0) return FSK_OK;
+  Params p;
+  memset(&p, 0, sizeof(p));
+  p.k = p.v = (const uint8_t*)pool;
+  p.k_s0 = p.v_s0 = stride_p * e; p.k_sh = p.v_sh = stride_h * e; p.k_st = p.v_st = stride_t * e;
+  p.lens = seq_lens; p.block_table = block_table; p.bt_sb = bt_stride_b; p.max_blocks = max_blocks;
+  p.num_pages = num_pages; p.page_size = page_size; p.B = batch; p.Hkv = num_kv_heads;
+  const int64_t rows = (int64_t)max_blocks * page_size;
+  dim3 grid((unsigned)(rows / 16), num_kv_heads, batch);
+  hipStream_t s = (hipStream_t)stream;
+  (void)hipGetLastError();
+  if (e == 2) {
+    if (head_dim == 64) hipLaunchKernelGGL((paged_gather_kernel<64, 2>), grid, dim3(64), 0, s, p, (uint8_t*)out, rows);
+    else if (head_dim == 128) hipLaunchKernelGGL((paged_gather_kernel<128, 2>), grid, dim3(64), 0, s, p, (uint8_t*)out, rows);
+    else hipLaunchKernelGGL((paged_gather_kernel<256, 2>), grid, dim3(64), 0, s, p, (uint8_t*)out, rows);
+  } else {
+    if (head_dim == 64) hipLaunchKernelGGL((paged_gather_kernel<64, 1>), grid, dim3(64), 0, s, p, (uint8_t*)out, rows);
+    else if (head_dim == 128) hipLaunchKernelGGL((paged_gather_kernel<128, 1>), grid, dim3(64), 0, s, p, (uint8_t*)out, rows);
+    else hipLaunchKernelGGL((paged_gather_kernel<256, 1>), grid, dim3(64), 0, s, p, (uint8_t*)out, rows);
+  }
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(FSK_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+  return FSK_OK;
+}
+
+int fsk_fp8_decode_table(uint16_t* out, void* stream) {
+  if (!out || !aligned(out, 8)) return fail(FSK_ERR_INVALID, "null or unaligned pointer");
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(fp8_table_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, (uint32_t*)out);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(FSK_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+  return FSK_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,367 @@
+"""GQA flash-decode entry points backed by the gfx950 HIP library.
+
+Each function keeps the name, positional signature, tensor layouts and return
+value of the reference entry point it replaces; new behaviour is only added
+through keyword-only arguments.  Every call validates its tensors, allocates
+the output and a split-KV workspace through torch's caching allocator, and
+launches the HIP kernels on torch's current stream (no host synchronisation,
+so the calls can be captured in a HIP graph).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _native as nat
+
+FP8_DTYPE = torch.float8_e4m3fn
+FP8_MAX = 448.0
+
+# Split counts fixed before graph capture, as in the reference modules
+# (fskernels/triton/triton_gqa_decode_hf.py:8-14, triton_gqa_decode_hf_fp8.py:156-161).
+_DECODE_NUM_SPLITS: int = 1
+_DECODE_NUM_SPLITS_FP8: int = 1
+
+
+def set_num_splits(n: int) -> None:
+    """Split-count hint for flash_decode_gqa_hf_dense_optimized.
+
+    The HIP kernels always split the KV sequence across the GPU with a device
+    work list; a value above 1 caps the number of splits per sequence (the
+    split size becomes ceil(S_max / n) rounded up to 32 tokens), 1 leaves the
+    split size to the library.  Mirrors fskernels/triton/triton_gqa_decode_hf.py:12-14.
+    """
+    global _DECODE_NUM_SPLITS
+    _DECODE_NUM_SPLITS = int(n)
+
+
+def set_num_splits_fp8(n: int) -> None:
+    """Split-count hint for flash_decode_gqa_hf_fp8 (see set_num_splits).
+
+    Mirrors fskernels/triton/triton_gqa_decode_hf_fp8.py:159-161.
+    """
+    global _DECODE_NUM_SPLITS_FP8
+    _DECODE_NUM_SPLITS_FP8 = int(n)
+
+
+def quantize_to_fp8(x: torch.Tensor):
+    """Per-tensor e4m3 quantisation: scale = max|x| / 448 (floored at 1e-12/448).
+
+    Same formula and return value as
+    fskernels/triton/triton_gqa_decode_hf_fp8.py:13-16: returns (x_fp8, scale)
+    with scale a 0-dim fp32 tensor on x's device.
+    """
+    scale = x.abs().max().clamp(min=1e-12) / FP8_MAX
+    x_fp8 = (x / scale).clamp(-FP8_MAX, FP8_MAX).to(FP8_DTYPE)
+    return x_fp8, scale
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+def _on_gpu(t: torch.Tensor, name: str, device: torch.device | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be on a GPU (HIP) device")
+    if device is not None and t.device != device:
+        raise RuntimeError(f"{name} is on {t.device}, expected {device}")
+
+
+def _inner_contig(t: torch.Tensor) -> torch.Tensor:
+    """Innermost dim contiguous with 16-byte aligned rows, else a packed copy."""
+    es = t.element_size()
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(
+        (s * es) % 16 == 0 for s in t.stride()[:-1])
+    return t if ok else t.contiguous()
+
+
+def _dtype_code(dt: torch.dtype, name: str) -> int:
+    try:
+        return nat.DTYPE_CODES[dt]
+    except KeyError:
+        raise NotImplementedError(f"{name}: unsupported dtype {dt}") from None
+
+
+def _int32(t: torch.Tensor, name: str, device: torch.device) -> torch.Tensor:
+    _on_gpu(t, name, device)
+    if t.dtype != torch.int32:
+        t = t.to(torch.int32)
+    return t.contiguous()
+
+
+def _scale_ptr(s, device, name):
+    """Scales are device fp32 scalars (0-dim or 1-element tensors)."""
+    if s is None:
+        return None, None
+    if not isinstance(s, torch.Tensor):
+        s = torch.tensor(float(s), dtype=torch.float32, device=device)
+    _on_gpu(s, name, device)
+    if s.numel() != 1:
+        raise ValueError(f"{name} must hold a single per-tensor scale")
+    s = s.reshape(()).to(torch.float32).contiguous()
+    return s, s.data_ptr()
+
+
+def _sinks(s_aux, hq, device):
+    if s_aux is None:
+        return None
+    _on_gpu(s_aux, "s_aux", device)
+    if s_aux.numel() != hq:
+        raise ValueError(f"s_aux must have num_q_heads={hq} entries, got {tuple(s_aux.shape)}")
+    return s_aux.reshape(hq).to(torch.float32).contiguous()
+
+
+def _sink_mode(mode: str) -> int:
+    try:
+        return nat.SINK_MODES[mode]
+    except KeyError:
+        raise ValueError(f"sink_mode must be 'exp' or 'linear', got {mode!r}") from None
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def _check_q(q: torch.Tensor):
+    _on_gpu(q, "q")
+    if q.dim() != 3:
+        raise ValueError(f"q must be [batch, num_q_heads, head_dim], got {tuple(q.shape)}")
+    return _inner_contig(q)
+
+
+# ---------------------------------------------------------------------------
+# varlen
+# ---------------------------------------------------------------------------
+def flash_decode_gqa_varlen(q, k_varlen, v_varlen, cu_seqlens_k, s_aux=None, *,
+                            sink_mode: str = "exp", k_scale=None, v_scale=None,
+                            out_dtype: torch.dtype | None = None, sm_scale: float | None = None,
+                            chunk_tokens: int = 0):
+    """Varlen GQA flash decode: out[b, h] = softmax(q[b,h] . K_b^T * sm_scale) V_b.
+
+    Reference: fskernels/triton/triton_gqa_decode.py:126-155 (and the positional
+    CUDA/TileLang variants fskernels/cuda/cuda_fd_gqa.py:14-15,
+    fskernels/tilelang/tilelang_gqa_decode.py:135-172).  q [B, Hq, D];
+    k_varlen / v_varlen [T, Hkv, D] packed by cu_seqlens_k int32 [B+1];
+    s_aux fp32 [Hq] sinks folded per ``sink_mode`` ("exp": sink logit, the
+    reference tests' oracle; "linear": added to the denominator as the
+    reference kernels do).  Returns a new [B, Hq, D] tensor of q's dtype
+    (``out_dtype`` overrides it).  fp8 K/V need k_scale / v_scale.
+    """
+    q = _check_q(q)
+    dev = q.device
+    for t, n in ((k_varlen, "k_varlen"), (v_varlen, "v_varlen")):
+        _on_gpu(t, n, dev)
+        if t.dim() != 3:
+            raise ValueError(f"{n} must be [total_tokens, num_kv_heads, head_dim]")
+    k = _inner_contig(k_varlen)
+    v = _inner_contig(v_varlen)
+    B, Hq, D = q.shape
+    T, Hkv, Dk = k.shape
+    if v.shape != k.shape or Dk != D:
+        raise ValueError("k_varlen / v_varlen shapes disagree with q")
+    cu = _int32(cu_seqlens_k, "cu_seqlens_k", dev)
+    if cu.numel() != B + 1:
+        raise ValueError(f"cu_seqlens_k must have batch+1={B + 1} entries")
+    sinks = _sinks(s_aux, Hq, dev)
+    ks, ksp = _scale_ptr(k_scale, dev, "k_scale")
+    vs, vsp = _scale_ptr(v_scale, dev, "v_scale")
+    odt = out_dtype or q.dtype
+    out = torch.empty((B, Hq, D), dtype=odt, device=dev)
+    scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
+    nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_VARLEN, B, Hq, Hkv, D, T, 16, chunk_tokens)
+    ws = _workspace(nbytes, dev)
+    lib = nat.load()
+    with torch.cuda.device(dev):
+        st = lib.fsk_decode_varlen(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            k.data_ptr(), k.stride(0), k.stride(1),
+            v.data_ptr(), v.stride(0), v.stride(1),
+            cu.data_ptr(), T, nat.ptr(sinks), _sink_mode(sink_mode), ksp, vsp,
+            out.data_ptr(), out.stride(0), out.stride(1),
+            B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_varlen"),
+            _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens,
+            nat.stream_handle(dev))
+    nat.check(st)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# dense (HF static cache)
+# ---------------------------------------------------------------------------
+def _dense(q, k_cache, v_cache, cache_lens, start_k_offsets, num_splits, *, q_scale=None,
+           k_scale=None, v_scale=None, out_dtype=None, s_aux=None, sink_mode="exp",
+           sm_scale=None, chunk_tokens=0):
+    q = _check_q(q)
+    dev = q.device
+    for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        _on_gpu(t, n, dev)
+        if t.dim() != 4:
+            raise ValueError(f"{n} must be [batch, num_kv_heads, max_seqlen, head_dim]")
+    k = _inner_contig(k_cache)
+    v = _inner_contig(v_cache)
+    B, Hq, D = q.shape
+    Bk, Hkv, S, Dk = k.shape
+    if v.shape != k.shape or Dk != D or Bk < B:
+        raise ValueError("k_cache / v_cache shapes disagree with q")
+    lens = _int32(cache_lens, "cache_lens", dev)
+    if lens.numel() < B:
+        raise ValueError("cache_lens must have one entry per sequence")
+    starts = None if start_k_offsets is None else _int32(start_k_offsets, "start_k_offsets", dev)
+    sinks = _sinks(s_aux, Hq, dev)
+    qs, qsp = _scale_ptr(q_scale, dev, "scale_q")
+    ks, ksp = _scale_ptr(k_scale, dev, "scale_k")
+    vs, vsp = _scale_ptr(v_scale, dev, "scale_v")
+    odt = out_dtype or q.dtype
+    out = torch.empty((B, Hq, D), dtype=odt, device=dev)
+    scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
+    if not chunk_tokens and num_splits and num_splits > 1:
+        chunk_tokens = max(32, -(-math.ceil(S / num_splits) // 32) * 32)
+    nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_DENSE, B, Hq, Hkv, D, S, 16, chunk_tokens)
+    ws = _workspace(nbytes, dev)
+    lib = nat.load()
+    with torch.cuda.device(dev):
+        st = lib.fsk_decode_dense(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+            v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), S,
+            lens.data_ptr(), nat.ptr(starts), nat.ptr(sinks), _sink_mode(sink_mode), qsp, ksp, vsp,
+            out.data_ptr(), out.stride(0), out.stride(1),
+            B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_cache"),
+            _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens,
+            nat.stream_handle(dev))
+    nat.check(st)
+    return out
+
+
+def flash_decode_gqa_hf_dense_optimized(q, k_cache, v_cache, cache_lens, start_k_offsets=None,
+                                        num_splits=None, *, s_aux=None, sink_mode: str = "exp",
+                                        sm_scale: float | None = None):
+    """Dense-cache split-KV decode over tokens [start_k_offsets[b], cache_lens[b]).
+
+    Reference: fskernels/triton/triton_gqa_decode_hf.py:146-211.  q [B, Hq, D];
+    k_cache / v_cache [B, Hkv, S_max, D] (HF static cache layout); cache_lens
+    int32 [B]; start_k_offsets int32 [B] (None: zeros).  ``num_splits``
+    (default: the set_num_splits value) is a split-count hint.
+    """
+    n = _DECODE_NUM_SPLITS if num_splits is None else num_splits
+    return _dense(q, k_cache, v_cache, cache_lens, start_k_offsets, n, s_aux=s_aux,
+                  sink_mode=sink_mode, sm_scale=sm_scale)
+
+
+def flash_decode_gqa_hf_fp8(q_fp8, k_cache_fp8, v_cache_fp8, cache_lens, scale_q, scale_k,
+                            scale_v, out_dtype):
+    """FP8 e4m3 dense decode with per-tensor scales.
+
+    Reference: fskernels/triton/triton_gqa_decode_hf_fp8.py:164-227.  q_fp8
+    [B, Hq, D] and the caches [B, Hkv, S_max, D] are float8_e4m3fn; scale_* are
+    0-dim fp32 device tensors (dequantised value = code * scale).  Q is
+    dequantised to fp16 as the reference does (:47-50); K/V are dequantised
+    exactly in registers and their scales applied in fp32.  Returns
+    [B, Hq, D] in ``out_dtype``.
+    """
+    return _dense(q_fp8, k_cache_fp8, v_cache_fp8, cache_lens, None, _DECODE_NUM_SPLITS_FP8,
+                  q_scale=scale_q, k_scale=scale_k, v_scale=scale_v, out_dtype=out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# paged
+# ---------------------------------------------------------------------------
+def paged_flash_decode(q, k_pool, v_pool, block_table, seq_lens, page_size, *, s_aux=None,
+                       k_scale=None, v_scale=None, out_dtype: torch.dtype | None = None,
+                       sink_mode: str = "exp", sm_scale: float | None = None,
+                       chunk_tokens: int = 0):
+    """Paged GQA decode through a block table.
+
+    Reference: fskernels/paged_attn/triton_paged_attn.py:96-125.  q [B, Hq, D];
+    k_pool / v_pool [P, Hkv, page_size, D] (e.g. PagedKVCache.k_pool[layer]);
+    block_table int32 [B, max_blocks] (logical page -> physical page, entries
+    past a sequence's last page are never read); seq_lens int32 [B].  The
+    keyword-only arguments add sinks and fp8 (e4m3) pools with per-tensor
+    scales, which the reference kernel does not have.
+    """
+    q = _check_q(q)
+    dev = q.device
+    for t, n in ((k_pool, "k_pool"), (v_pool, "v_pool")):
+        _on_gpu(t, n, dev)
+        if t.dim() != 4:
+            raise ValueError(f"{n} must be [num_pages, num_kv_heads, page_size, head_dim]")
+    k = _inner_contig(k_pool)
+    v = _inner_contig(v_pool)
+    B, Hq, D = q.shape
+    P, Hkv, PS, Dk = k.shape
+    if v.shape != k.shape or Dk != D:
+        raise ValueError("k_pool / v_pool shapes disagree with q")
+    if int(page_size) != PS:
+        raise ValueError(f"page_size={page_size} but the pools hold {PS}-token pages")
+    _on_gpu(block_table, "block_table", dev)
+    if block_table.dim() != 2 or block_table.shape[0] < B:
+        raise ValueError("block_table must be [batch, max_blocks]")
+    bt = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
+    if bt.stride(1) != 1:
+        bt = bt.contiguous()
+    lens = _int32(seq_lens, "seq_lens", dev)
+    if lens.numel() < B:
+        raise ValueError("seq_lens must have one entry per sequence")
+    sinks = _sinks(s_aux, Hq, dev)
+    ks, ksp = _scale_ptr(k_scale, dev, "k_scale")
+    vs, vsp = _scale_ptr(v_scale, dev, "v_scale")
+    odt = out_dtype or q.dtype
+    out = torch.empty((B, Hq, D), dtype=odt, device=dev)
+    scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
+    max_blocks = bt.shape[1]
+    nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_PAGED, B, Hq, Hkv, D, max_blocks, PS, chunk_tokens)
+    ws = _workspace(nbytes, dev)
+    lib = nat.load()
+    with torch.cuda.device(dev):
+        st = lib.fsk_decode_paged(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+            v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+            bt.data_ptr(), bt.stride(0), max_blocks, lens.data_ptr(), P, PS,
+            nat.ptr(sinks), _sink_mode(sink_mode), ksp, vsp,
+            out.data_ptr(), out.stride(0), out.stride(1),
+            B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_pool"),
+            _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens,
+            nat.stream_handle(dev))
+    nat.check(st)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# debug exports
+# ---------------------------------------------------------------------------
+def paged_gather(pool, block_table, seq_lens):
+    """Dense [B, Hkv, max_blocks*page_size, D] copy of a paged pool, read through
+    the decode kernels' page-addressing routine (rows past seq_lens are zero)."""
+    _on_gpu(pool, "pool")
+    dev = pool.device
+    pool = _inner_contig(pool)
+    P, Hkv, PS, D = pool.shape
+    bt = _int32(block_table, "block_table", dev)
+    lens = _int32(seq_lens, "seq_lens", dev)
+    B, MB = bt.shape
+    out = torch.empty((B, Hkv, MB * PS, D), dtype=pool.dtype, device=dev)
+    lib = nat.load()
+    with torch.cuda.device(dev):
+        st = lib.fsk_paged_gather(pool.data_ptr(), pool.stride(0), pool.stride(1), pool.stride(2),
+                                  bt.data_ptr(), bt.stride(0), MB, lens.data_ptr(), P, PS, B, Hkv,
+                                  D, _dtype_code(pool.dtype, "pool"), out.data_ptr(),
+                                  nat.stream_handle(dev))
+    nat.check(st)
+    return out
+
+
+def fp8_decode_table(device="cuda"):
+    """[2, 256] fp32: every e4m3 code through the kernels' f16 and bf16 routes
+    (the kernel returns the 16-bit patterns; they are widened here)."""
+    dev = torch.device(device)
+    out = torch.empty(512, dtype=torch.int16, device=dev)
+    lib = nat.load()
+    with torch.cuda.device(dev):
+        st = lib.fsk_fp8_decode_table(out.data_ptr(), nat.stream_handle(dev))
+    nat.check(st)
+    bits = out.cpu()
+    return torch.stack([bits[:256].view(torch.float16).to(torch.float32),
+                        bits[256:].view(torch.bfloat16).to(torch.float32)])

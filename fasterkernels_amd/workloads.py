@@ -1,0 +1,195 @@
+"""Seeded synthetic decode workloads (the benchmark configurations).
+
+Draw order with one torch.Generator: lengths -> block-table permutation -> Q ->
+K -> V -> s_aux.  Paged pools hold the pages the sequences need plus 10 %
+free pages; a seeded permutation of the pool assigns physical pages, so pages
+of one sequence are scattered.  Every slot of the pool (including free pages
+and the tail of a partial last page) holds random data, so a kernel that
+reads past a sequence end produces wrong results.
+
+fp8 pools are generated as N(0,1) fp32 and quantised per tensor with
+scale = max|x| / 448 (fskernels/triton/triton_gqa_decode_hf_fp8.py:13-16).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+PAGE = 16
+
+# name -> configuration (shapes from the benchmark definition)
+CONFIGS = {
+    # headline: paged fp16, B=4, 32K context
+    "M0": dict(layout="paged", q="f16", kv="f16", out="f16", B=4, Hq=32, Hkv=8, D=128,
+               lens=("fixed", 32768), sinks=False, seed=100),
+    # varlen fp16, lengths U[1, 2048], no sinks
+    "C1": dict(layout="varlen", q="f16", kv="f16", out="f16", B=4, Hq=32, Hkv=8, D=128,
+               lens=("uniform", 1, 2048), sinks=False, seed=101),
+    # varlen fp16, 32K, N(0,1) sinks
+    "C2": dict(layout="varlen", q="f16", kv="f16", out="f16", B=4, Hq=32, Hkv=8, D=128,
+               lens=("fixed", 32768), sinks=True, seed=102),
+    # paged fp16, B=32, lengths U[1024, 16384]
+    "C3": dict(layout="paged", q="f16", kv="f16", out="f16", B=32, Hq=32, Hkv=8, D=128,
+               lens=("uniform", 1024, 16384), sinks=False, seed=103),
+    # paged e4m3 KV, bf16 Q and output, 8K
+    "C4": dict(layout="paged", q="bf16", kv="e4m3", out="bf16", B=4, Hq=32, Hkv=8, D=128,
+               lens=("fixed", 8192), sinks=False, seed=104),
+    # paged e4m3 KV + sinks, B=64, lognormal lengths
+    "C5": dict(layout="paged", q="bf16", kv="e4m3", out="bf16", B=64, Hq=32, Hkv=8, D=128,
+               lens=("lognormal", math.log(4096.0), 1.0, 16, 32768), sinks=True, seed=105),
+}
+
+DTYPES = {"f16": torch.float16, "bf16": torch.bfloat16, "e4m3": torch.float8_e4m3fn,
+          "f32": torch.float32}
+
+
+@dataclass
+class Workload:
+    name: str
+    layout: str
+    B: int
+    Hq: int
+    Hkv: int
+    D: int
+    lens: list
+    q: torch.Tensor
+    k: torch.Tensor              # varlen [T,Hkv,D] / paged pool [P,Hkv,16,D]
+    v: torch.Tensor
+    cu_seqlens: torch.Tensor | None = None
+    block_table: torch.Tensor | None = None
+    seq_lens: torch.Tensor | None = None
+    s_aux: torch.Tensor | None = None
+    k_scale: torch.Tensor | None = None
+    v_scale: torch.Tensor | None = None
+    out_dtype: torch.dtype = torch.float16
+    meta: dict = field(default_factory=dict)
+
+    @property
+    def total_tokens(self) -> int:
+        return int(sum(self.lens))
+
+    def to(self, device) -> "Workload":
+        def mv(t):
+            return None if t is None else t.to(device)
+        return Workload(self.name, self.layout, self.B, self.Hq, self.Hkv, self.D, list(self.lens),
+                        mv(self.q), mv(self.k), mv(self.v), mv(self.cu_seqlens),
+                        mv(self.block_table), mv(self.seq_lens), mv(self.s_aux), mv(self.k_scale),
+                        mv(self.v_scale), self.out_dtype, dict(self.meta))
+
+    def algorithmic_bytes(self) -> int:
+        """Bytes a decode step must move: valid-token K+V, Q, output, the block
+        table entries used, lengths, sinks and scales."""
+        kv_elem = self.k.element_size()
+        n = self.total_tokens * self.Hkv * self.D * 2 * kv_elem
+        n += self.B * self.Hq * self.D * (self.q.element_size() + DTYPES_SIZE[self.out_dtype])
+        if self.layout == "paged":
+            n += 4 * sum((L + PAGE - 1) // PAGE for L in self.lens) + 4 * self.B
+        else:
+            n += 4 * (self.B + 1)
+        if self.s_aux is not None:
+            n += 4 * self.Hq
+        if self.k_scale is not None:
+            n += 8
+        return n
+
+    def flops(self) -> int:
+        return 4 * self.D * self.Hq * self.total_tokens
+
+
+DTYPES_SIZE = {torch.float16: 2, torch.bfloat16: 2, torch.float32: 4}
+
+
+def _lengths(spec, B, g):
+    kind = spec[0]
+    if kind == "fixed":
+        return [int(spec[1])] * B
+    if kind == "uniform":
+        return torch.randint(int(spec[1]), int(spec[2]) + 1, (B,), generator=g).tolist()
+    if kind == "lognormal":
+        mu, sigma, lo, hi = spec[1:]
+        z = torch.randn(B, generator=g, dtype=torch.float64)
+        return [int(min(max(round(math.exp(mu + sigma * float(x))), lo), hi)) for x in z]
+    if kind == "list":
+        return [int(x) for x in spec[1]]
+    raise ValueError(kind)
+
+
+def _randn(shape, g, device):
+    if device is None or torch.device(device).type == "cpu":
+        return torch.randn(*shape, generator=g)
+    return torch.randn(*shape, generator=g, device=device)
+
+
+def _quantize(x):
+    amax = x.abs().max().clamp(min=1e-12)
+    scale = (amax / 448.0).to(torch.float32)
+    return (x / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn), scale
+
+
+def make(name: str = "M0", *, device=None, seed: int | None = None, overrides: dict | None = None,
+         gen_device=None) -> Workload:
+    """Builds a workload.  ``overrides`` replaces config keys (e.g. smaller
+    ``B`` or ``lens`` for tests).  Random draws use a CPU generator unless
+    ``gen_device`` names a GPU (faster for large benchmark inputs, different
+    values)."""
+    cfg = dict(CONFIGS[name])
+    if overrides:
+        cfg.update(overrides)
+    seed = cfg["seed"] if seed is None else seed
+    gdev = torch.device(gen_device) if gen_device is not None else torch.device("cpu")
+    g = torch.Generator().manual_seed(seed)          # lengths, permutation (and data on CPU)
+    gd = g if gdev.type == "cpu" else torch.Generator(device=gdev).manual_seed(seed)
+    B, Hq, Hkv, D = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["D"]
+    lens = _lengths(cfg["lens"], B, g)
+    layout = cfg["layout"]
+    qdt, kvdt, odt = DTYPES[cfg["q"]], DTYPES[cfg["kv"]], DTYPES[cfg["out"]]
+    rd = None if gdev.type == "cpu" else gdev
+    wl_meta = {"config": name, "seed": seed}
+    cu = bt = sl = None
+    if layout == "paged":
+        npages = [(L + PAGE - 1) // PAGE for L in lens]
+        total = sum(npages)
+        P = max(total + int(math.ceil(0.1 * total)), 1)
+        perm = torch.randperm(P, generator=g).tolist()
+        max_blocks = int(cfg.get("max_blocks") or max(max(npages), 1))
+        bt = torch.full((B, max_blocks), -1, dtype=torch.int32)
+        off = 0
+        for b, n in enumerate(npages):
+            bt[b, :n] = torch.tensor(perm[off:off + n], dtype=torch.int32)
+            off += n
+        sl = torch.tensor(lens, dtype=torch.int32)
+        kv_shape = (P, Hkv, PAGE, D)
+        wl_meta.update(num_pages=P, max_blocks=max_blocks)
+    else:
+        T = sum(lens)
+        cu = torch.zeros(B + 1, dtype=torch.int32)
+        cu[1:] = torch.cumsum(torch.tensor(lens, dtype=torch.int64), 0).to(torch.int32)
+        kv_shape = (T, Hkv, D)
+    q = _randn((B, Hq, D), gd, rd).to(qdt)
+    kf = _randn(kv_shape, gd, rd)
+    vf = _randn(kv_shape, gd, rd)
+    ks = vs = None
+    if kvdt == torch.float8_e4m3fn:
+        k, ks = _quantize(kf)
+        v, vs = _quantize(vf)
+    else:
+        k, v = kf.to(kvdt), vf.to(kvdt)
+    del kf, vf
+    s_aux = _randn((Hq,), gd, rd).to(torch.float32) if cfg["sinks"] else None
+    wl = Workload(name, layout, B, Hq, Hkv, D, lens, q, k, v, cu, bt, sl, s_aux, ks, vs, odt, wl_meta)
+    return wl.to(device) if device is not None else wl
+
+
+def run(wl: Workload, *, sink_mode: str = "exp", chunk_tokens: int = 0):
+    """One decode step of ``wl`` through the HIP entry points."""
+    from .hip import decode as dec
+    if wl.layout == "paged":
+        return dec.paged_flash_decode(wl.q, wl.k, wl.v, wl.block_table, wl.seq_lens, PAGE,
+                                      s_aux=wl.s_aux, k_scale=wl.k_scale, v_scale=wl.v_scale,
+                                      out_dtype=wl.out_dtype, sink_mode=sink_mode,
+                                      chunk_tokens=chunk_tokens)
+    return dec.flash_decode_gqa_varlen(wl.q, wl.k, wl.v, wl.cu_seqlens, wl.s_aux,
+                                       sink_mode=sink_mode, k_scale=wl.k_scale, v_scale=wl.v_scale,
+                                       out_dtype=wl.out_dtype, chunk_tokens=chunk_tokens)

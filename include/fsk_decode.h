@@ -1,0 +1,188 @@
+/*
+ * fsk_decode.h -- C ABI of the MI355X (gfx950) GQA flash-decode library.
+ *
+ * One query token per sequence attends over that sequence's KV cache.  Query
+ * head h reads KV head h / (num_q_heads / num_kv_heads).  Three KV layouts are
+ * supported, each with fp16 / bf16 / fp8-e4m3 KV:
+ *
+ *   varlen : k[T, Hkv, D], sequence b owns rows [cu_seqlens[b], cu_seqlens[b+1])
+ *   paged  : k_pool[P, Hkv, page_size, D], token t of sequence b lives in page
+ *            block_table[b, t / page_size] at row t % page_size
+ *   dense  : k[B, Hkv, S_max, D], sequence b attends rows
+ *            [start_offsets[b], cache_lens[b])
+ *
+ * Every entry point validates its arguments on the host before any HIP call,
+ * returns FSK_OK (0) or a negative status, and keeps a thread-local message
+ * readable through fsk_last_error().  The library never allocates device
+ * memory in these entry points: outputs and the split-KV workspace are passed
+ * in (size it with fsk_workspace_bytes).  Work is enqueued on `stream` without
+ * host synchronisation, so every call can be captured into a HIP graph.
+ *
+ * Strides are in ELEMENTS of the tensor they describe; the innermost (head_dim)
+ * stride must be 1.  Lengths, offsets, block tables and scales are read on the
+ * device; out-of-range values are clamped so that no access leaves the tensors
+ * described by the sizes passed here.
+ */
+#ifndef FSK_DECODE_H
+#define FSK_DECODE_H
+
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define FSK_API __attribute__((visibility("default")))
+#else
+#define FSK_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define FSK_OK 0
+#define FSK_ERR_INVALID (-1)     /* bad argument: null pointer, shape, stride */
+#define FSK_ERR_UNSUPPORTED (-2) /* valid but not implemented (head_dim, dtype) */
+#define FSK_ERR_WORKSPACE (-3)   /* workspace missing or too small */
+#define FSK_ERR_HIP (-4)         /* HIP runtime error at launch */
+
+/* Element types. */
+#define FSK_F16 0
+#define FSK_BF16 1
+#define FSK_F32 2
+#define FSK_E4M3 3 /* OCP float8 e4m3fn (torch.float8_e4m3fn) */
+
+/* Sink folding.  With s = q.k * sm_scale over the sequence and a per-q-head
+ * sink value z:
+ *   FSK_SINK_EXP    : out = sum_t e^{s_t} v_t / (sum_t e^{s_t} + e^{z})
+ *                     (z is an extra logit with a zero value vector; the
+ *                     semantics of the reference's test oracles)
+ *   FSK_SINK_LINEAR : out = sum_t e^{s_t - m} v_t / (sum_t e^{s_t - m} + z),
+ *                     m = max_t s_t (the fold done by the reference kernels)
+ */
+#define FSK_SINK_EXP 0
+#define FSK_SINK_LINEAR 1
+
+/* KV layouts (argument of fsk_workspace_bytes). */
+#define FSK_LAYOUT_VARLEN 0
+#define FSK_LAYOUT_PAGED 1
+#define FSK_LAYOUT_DENSE 2
+
+/* Message of the last failed call on this thread ("" if none). */
+FSK_API const char *fsk_last_error(void);
+
+/* Library ABI version, currently 1. */
+FSK_API int fsk_version(void);
+
+/* Bytes of device workspace a decode call needs.
+ *   kv_extent: varlen -> total rows T of k/v;
+ *              paged  -> block_table width (max blocks per sequence);
+ *              dense  -> S_max (dim 2 of the cache).
+ *   page_size: paged layout only (ignored otherwise).
+ *   chunk_tokens: split size in tokens (multiple of 32) or 0 for the default
+ *              the library would pick for this shape.
+ * Returns the byte count (> 0) or a negative status. */
+FSK_API int64_t fsk_workspace_bytes(int layout, int batch, int num_q_heads, int num_kv_heads,
+                            int head_dim, int64_t kv_extent, int page_size,
+                            int chunk_tokens);
+
+/* Varlen GQA decode.
+ * Replaces: fskernels/triton/triton_gqa_decode.py:126-155 (flash_decode_gqa_varlen
+ *           + _flash_decode_gqa_varlen_kernel launch, :142-154) and
+ *           fskernels/cuda/flash_decode_cuda.cu:168-188 (launch_flash_decode_gqa).
+ * q [B, Hq, D], k/v [T, Hkv, D], cu_seqlens int32 [B+1], s_aux fp32 [Hq] or
+ * NULL, out [B, Hq, D].  k/v may be fp16, bf16 or e4m3 (then k_scale/v_scale are
+ * device fp32 scalars, dequantised value = code * scale). */
+FSK_API int fsk_decode_varlen(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                      const void *k, int64_t k_stride_t, int64_t k_stride_h,
+                      const void *v, int64_t v_stride_t, int64_t v_stride_h,
+                      const int32_t *cu_seqlens, int64_t total_tokens,
+                      const float *s_aux, int sink_mode,
+                      const float *k_scale, const float *v_scale,
+                      void *out, int64_t o_stride_b, int64_t o_stride_h,
+                      int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                      int q_dtype, int kv_dtype, int out_dtype, float sm_scale,
+                      void *workspace, int64_t workspace_bytes, int chunk_tokens,
+                      void *stream);
+
+/* Paged GQA decode.
+ * Replaces: fskernels/paged_attn/triton_paged_attn.py:96-125 (paged_flash_decode
+ *           + _paged_flash_decode_kernel launch, :112-124).
+ * k_pool/v_pool [P, Hkv, page_size, D] (a per-layer view of PagedKVCache's
+ * pools, fskernels/paged_attn/paged_kv_cache.py:46-51), block_table int32
+ * [B, max_blocks] (row stride bt_stride_b), seq_lens int32 [B].  page_size must
+ * be a multiple of 16. */
+FSK_API int fsk_decode_paged(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                     const void *k_pool, int64_t k_stride_p, int64_t k_stride_h,
+                     int64_t k_stride_t,
+                     const void *v_pool, int64_t v_stride_p, int64_t v_stride_h,
+                     int64_t v_stride_t,
+                     const int32_t *block_table, int64_t bt_stride_b, int max_blocks,
+                     const int32_t *seq_lens, int num_pages, int page_size,
+                     const float *s_aux, int sink_mode,
+                     const float *k_scale, const float *v_scale,
+                     void *out, int64_t o_stride_b, int64_t o_stride_h,
+                     int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                     int q_dtype, int kv_dtype, int out_dtype, float sm_scale,
+                     void *workspace, int64_t workspace_bytes, int chunk_tokens,
+                     void *stream);
+
+/* Dense (HF static cache) GQA decode.
+ * Replaces: fskernels/triton/triton_gqa_decode_hf.py:146-211
+ *           (flash_decode_gqa_hf_dense_optimized: partial :186-199 + reduce
+ *           :201-209) and fskernels/triton/triton_gqa_decode_hf_fp8.py:164-227
+ *           (flash_decode_gqa_hf_fp8; q_dtype FSK_E4M3 with q_scale reproduces
+ *           its q = fp16(fp32(q8) * scale_q), :47-50).
+ * k/v [B, Hkv, S_max, D]; cache_lens int32 [B]; start_offsets int32 [B] or
+ * NULL (all zero). */
+FSK_API int fsk_decode_dense(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                     const void *k, int64_t k_stride_b, int64_t k_stride_h,
+                     int64_t k_stride_t,
+                     const void *v, int64_t v_stride_b, int64_t v_stride_h,
+                     int64_t v_stride_t, int64_t max_seqlen,
+                     const int32_t *cache_lens, const int32_t *start_offsets,
+                     const float *s_aux, int sink_mode, const float *q_scale,
+                     const float *k_scale, const float *v_scale,
+                     void *out, int64_t o_stride_b, int64_t o_stride_h,
+                     int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                     int q_dtype, int kv_dtype, int out_dtype, float sm_scale,
+                     void *workspace, int64_t workspace_bytes, int chunk_tokens,
+                     void *stream);
+
+/* Debug: gather a paged pool into a dense [B, Hkv, max_blocks*page_size, D]
+ * tensor through the decode kernels' own page-addressing routine; rows at or
+ * past seq_lens[b] are written as zero.  Bit-exact copy of the element bytes.
+ * Checks the page-addressing contract of
+ * fskernels/paged_attn/triton_paged_attn.py:57-69. */
+FSK_API int fsk_paged_gather(const void *pool, int64_t stride_p, int64_t stride_h,
+                     int64_t stride_t, const int32_t *block_table,
+                     int64_t bt_stride_b, int max_blocks, const int32_t *seq_lens,
+                     int num_pages, int page_size, int batch, int num_kv_heads,
+                     int head_dim, int dtype, void *out, void *stream);
+
+/* Debug: decode all 256 e4m3 codes with the kernels' in-register dequant
+ * routines and store the raw 16-bit results.  out[0..255]: fp16 bit pattern
+ * of code i; out[256..511]: bf16 bit pattern of code i (out 8-byte aligned).
+ * Widened to fp32 on the host, both must equal the e4m3fn -> fp32 cast the
+ * reference relies on (fskernels/triton/triton_gqa_decode_hf_fp8.py:71-73,
+ * :90-92). */
+FSK_API int fsk_fp8_decode_table(uint16_t *out, void *stream);
+
+/* Tuning knobs for benchmarking sweeps ("chunk_tokens", "waves_per_cu").
+ * Returns FSK_OK or FSK_ERR_INVALID for an unknown name or bad value. */
+FSK_API int fsk_set_option(const char *name, int64_t value);
+
+/* Profiling hook (no counterpart in the reference; used by the benchmark).
+ * While enabled, every decode call records HIP events on its stream before the
+ * split-KV partial kernel, between it and the reduce kernel, and after the
+ * reduce kernel.  Not for use under HIP graph capture.  fsk_kernel_timing()
+ * waits for the recorded events, returns the summed partial-kernel and
+ * partial+reduce milliseconds and the number of decode calls, and clears the
+ * record.  Disabling also clears it. */
+FSK_API int fsk_enable_kernel_timing(int enable);
+FSK_API int fsk_kernel_timing(double *partial_ms, double *total_ms, int64_t *calls);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FSK_DECODE_H */

@@ -1,0 +1,262 @@
+"""CPU oracle for the GQA flash-decode hot path (numpy, float64).
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this module, and only as the checker or the timed
+CPU baseline.  The product path (fasterkernels_amd) never imports it and has no
+CPU fallback.
+
+It restates, in plain numpy, what the reference computes on the decode path:
+
+* GQA attention for one query token per sequence: query head h reads KV head
+  h // (Hq / Hkv) (repeat_kv, tests/test_triton_fd_gqa.py:8-13; head mapping
+  fskernels/triton/triton_gqa_decode.py:53-56), scores q.k * sm_scale with
+  sm_scale = 1/sqrt(D) (:70-71, :86-87), softmax over the valid tokens.
+* Sinks, two semantics (a per-query-head value z):
+    "exp"    -- z is an extra logit with a zero value vector:
+                p_t = e^{s_t - M} / (sum e^{s - M} + e^{z - M}), M = max(max s, z)
+                (tests/test_triton_fd_gqa.py:117-132, :27-33)
+    "linear" -- z is added to the softmax denominator relative to m = max s:
+                den = sum e^{s - m} + z
+                (fskernels/triton/triton_gqa_decode.py:111-118;
+                 fskernels/cuda/flash_decode_cuda.cu:151-153)
+* Varlen packing through cu_seqlens (triton_gqa_decode.py:66-68, :81).
+* Paged addressing: token t of sequence b is pool[block_table[b, t // ps], h,
+  t % ps] (fskernels/paged_attn/triton_paged_attn.py:57-69), tokens >= seq_len
+  masked (:71-79).
+* Dense HF cache: tokens [start_k_offsets[b], cache_lens[b]) of
+  k[b, h, :, :] (fskernels/triton/triton_gqa_decode_hf.py:46-54, :62-64).
+* Split-KV partials and their log-sum-exp merge
+  (triton_gqa_decode_hf.py:52-54, :90-99, :103-137).
+* e4m3fn (OCP FP8, torch.float8_e4m3fn) decoding from the format definition,
+  encoding with round-to-nearest-even, and the per-tensor quantiser
+  scale = max|x|.clamp(1e-12) / 448, x8 = e4m3(clamp(x / scale, +-448))
+  (fskernels/triton/triton_gqa_decode_hf_fp8.py:9-16); dequantised values are
+  fp32(code) * scale (:47-50, :71-73, :90-92).
+
+Every function is pinned by tests/test_oracle.py (closed forms, a library
+routine -- torch's scaled_dot_product_attention and its float8 cast --,
+brute-force loops on tiny inputs, committed golden vectors and planted
+mistakes that must be caught).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+E4M3_MAX = 448.0
+
+
+# ---------------------------------------------------------------------------
+# e4m3fn codec (OCP OFP8 E4M3: bias 7, no infinities, S.1111.111 = NaN)
+# ---------------------------------------------------------------------------
+def e4m3_decode(codes) -> np.ndarray:
+    """uint8 codes -> float32 values, from the bit-level definition."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    exp = (c >> 3) & 0xF
+    man = c & 0x7
+    normal = (1.0 + man / 8.0) * np.power(2.0, exp - 7.0)
+    subnormal = (man / 8.0) * 2.0 ** -6
+    val = sign * np.where(exp == 0, subnormal, normal)
+    val = np.where((c & 0x7F) == 0x7F, np.nan, val)
+    return val.astype(np.float32)
+
+
+_E4M3_POS = e4m3_decode(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)  # codes 0..126
+
+
+def e4m3_encode(x) -> np.ndarray:
+    """float -> uint8 code, round to nearest (ties to even code), NaN -> 0x7F.
+
+    Magnitudes above 448 are not clamped here (the quantiser clamps first,
+    triton_gqa_decode_hf_fp8.py:15); they round to 448 if below the 464
+    midpoint, else encode NaN as torch's float8_e4m3fn cast does.
+    """
+    x = np.asarray(x, dtype=np.float64)
+    a = np.abs(x)
+    idx = np.searchsorted(_E4M3_POS, a, side="left")
+    idx = np.clip(idx, 1, len(_E4M3_POS) - 1)
+    lo = _E4M3_POS[idx - 1]
+    hi = _E4M3_POS[idx]
+    pick_hi = (a - lo > hi - a) | ((a - lo == hi - a) & ((idx % 2) == 0))
+    code = np.where(pick_hi, idx, idx - 1)
+    code = np.where(a <= _E4M3_POS[0], 0, code)
+    code = np.where(a >= 464.0, 0x7F, code)  # past the last midpoint: NaN
+    code = np.where(np.isnan(a), 0x7F, code)
+    sign = np.where(np.signbit(x), 0x80, 0)
+    return (code | sign).astype(np.uint8)
+
+
+def quantize_to_fp8(x):
+    """(codes uint8, scale float32) as the reference quantiser computes them."""
+    x32 = np.asarray(x, dtype=np.float32)
+    amax = np.float32(np.abs(x32).max()) if x32.size else np.float32(0)
+    scale = np.float32(max(amax, np.float32(1e-12)) / np.float32(E4M3_MAX))
+    y = np.clip(x32 / scale, -E4M3_MAX, E4M3_MAX).astype(np.float32)
+    return e4m3_encode(y), scale
+
+
+def dequantize_fp8(codes, scale) -> np.ndarray:
+    return (e4m3_decode(codes) * np.float32(scale)).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+def attend(q, k, v, sink=None, sink_mode: str = "exp", sm_scale: float | None = None):
+    """One decode step of one sequence.
+
+    q [Hq, D]; k, v [L, Hkv, D]; sink [Hq] or None.  Returns [Hq, D] float64.
+    Query head h uses KV head h // (Hq // Hkv).  L = 0 gives NaN without a sink
+    (0/0, as the reference kernels produce) and the sink-only result with one.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    Hq, D = q.shape
+    L, Hkv, _ = k.shape
+    G = Hq // Hkv
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
+    out = np.empty((Hq, D), dtype=np.float64)
+    for kvh in range(Hkv):
+        qs = q[kvh * G:(kvh + 1) * G]                  # [G, D]
+        s = (qs @ k[:, kvh, :].T) * scale              # [G, L]
+        m = s.max(axis=1, keepdims=True) if L else np.full((G, 1), -np.inf)
+        if sink is not None and sink_mode == "exp":
+            z = np.asarray(sink, dtype=np.float64)[kvh * G:(kvh + 1) * G, None]
+            M = np.maximum(m, z)
+            e = np.exp(s - M)
+            den = e.sum(axis=1, keepdims=True) + np.exp(z - M)
+        else:
+            with np.errstate(invalid="ignore"):
+                e = np.exp(s - m)
+            den = e.sum(axis=1, keepdims=True)
+            if sink is not None:
+                if sink_mode != "linear":
+                    raise ValueError(f"unknown sink_mode {sink_mode!r}")
+                den = den + np.asarray(sink, dtype=np.float64)[kvh * G:(kvh + 1) * G, None]
+        with np.errstate(invalid="ignore", divide="ignore"):
+            out[kvh * G:(kvh + 1) * G] = (e @ v[:, kvh, :]) / den
+    return out
+
+
+def decode_varlen(q, k, v, cu_seqlens, s_aux=None, sink_mode="exp", sm_scale=None):
+    """q [B, Hq, D]; k, v [T, Hkv, D]; cu_seqlens [B+1] -> [B, Hq, D]."""
+    q = np.asarray(q)
+    cu = np.asarray(cu_seqlens, dtype=np.int64)
+    return np.stack([attend(q[b], k[cu[b]:cu[b + 1]], v[cu[b]:cu[b + 1]], s_aux, sink_mode, sm_scale)
+                     for b in range(q.shape[0])])
+
+
+def paged_rows(pool, block_table, b: int, length: int):
+    """Rows [0, length) of sequence b gathered from pool [P, Hkv, ps, D] -> [L, Hkv, D]."""
+    pool = np.asarray(pool)
+    ps = pool.shape[2]
+    t = np.arange(length)
+    pages = np.asarray(block_table)[b, t // ps]
+    return pool[pages, :, t % ps, :]
+
+
+def paged_gather(pool, block_table, seq_lens):
+    """Dense [B, Hkv, max_blocks*ps, D] copy of a pool; rows >= seq_len are zero."""
+    pool = np.asarray(pool)
+    bt = np.asarray(block_table)
+    B, MB = bt.shape
+    P, Hkv, ps, D = pool.shape
+    out = np.zeros((B, Hkv, MB * ps, D), dtype=pool.dtype)
+    for b in range(B):
+        L = int(seq_lens[b])
+        out[b, :, :L, :] = paged_rows(pool, bt, b, L).transpose(1, 0, 2)
+    return out
+
+
+def decode_paged(q, k_pool, v_pool, block_table, seq_lens, s_aux=None, sink_mode="exp",
+                 k_scale=None, v_scale=None, sm_scale=None):
+    """q [B, Hq, D]; pools [P, Hkv, ps, D] (float values, or uint8 e4m3 codes when
+    k_scale / v_scale are given) -> [B, Hq, D]."""
+    q = np.asarray(q)
+    outs = []
+    for b in range(q.shape[0]):
+        L = int(seq_lens[b])
+        k = paged_rows(k_pool, block_table, b, L)
+        v = paged_rows(v_pool, block_table, b, L)
+        if k_scale is not None:
+            k = dequantize_fp8(k, k_scale)
+        if v_scale is not None:
+            v = dequantize_fp8(v, v_scale)
+        outs.append(attend(q[b], k, v, s_aux, sink_mode, sm_scale))
+    return np.stack(outs)
+
+
+def decode_dense(q, k, v, cache_lens, start_offsets=None, s_aux=None, sink_mode="exp",
+                 k_scale=None, v_scale=None, sm_scale=None):
+    """q [B, Hq, D]; k, v [B, Hkv, S, D] -> [B, Hq, D] over rows [start, len)."""
+    q = np.asarray(q)
+    outs = []
+    for b in range(q.shape[0]):
+        e = int(cache_lens[b])
+        s = 0 if start_offsets is None else int(start_offsets[b])
+        kb = np.asarray(k)[b, :, s:e, :].transpose(1, 0, 2)
+        vb = np.asarray(v)[b, :, s:e, :].transpose(1, 0, 2)
+        if k_scale is not None:
+            kb = dequantize_fp8(kb, k_scale)
+        if v_scale is not None:
+            vb = dequantize_fp8(vb, v_scale)
+        outs.append(attend(q[b], kb, vb, s_aux, sink_mode, sm_scale))
+    return np.stack(outs)
+
+
+# ---------------------------------------------------------------------------
+# split-KV partials and their merge
+# ---------------------------------------------------------------------------
+def partials(q, k, v, n_splits: int, sm_scale=None):
+    """Split the L tokens into n_splits ranges of ceil(L/n) tokens and return
+    (acc [n, Hq, D] unnormalised, m [n, Hq], l [n, Hq]) per range, as the
+    dense split kernel produces them (triton_gqa_decode_hf.py:52-54, :90-99).
+    Empty ranges give m = -inf, l = 0, acc = 0."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    Hq, D = q.shape
+    L, Hkv, _ = k.shape
+    G = Hq // Hkv
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
+    tps = -(-L // n_splits) if L else 0
+    acc = np.zeros((n_splits, Hq, D))
+    m = np.full((n_splits, Hq), -np.inf)
+    l = np.zeros((n_splits, Hq))
+    for i in range(n_splits):
+        lo, hi = i * tps, min((i + 1) * tps, L)
+        if lo >= hi:
+            continue
+        for h in range(Hq):
+            s = (k[lo:hi, h // G, :] @ q[h]) * scale
+            m[i, h] = s.max()
+            e = np.exp(s - m[i, h])
+            l[i, h] = e.sum()
+            acc[i, h] = e @ v[lo:hi, h // G, :]
+    return acc, m, l
+
+
+def merge_partials(acc, m, l, sink=None, sink_mode="exp"):
+    """Log-sum-exp merge (triton_gqa_decode_hf.py:117-135) plus the sink fold."""
+    acc = np.asarray(acc, dtype=np.float64)
+    m = np.asarray(m, dtype=np.float64)
+    l = np.asarray(l, dtype=np.float64)
+    M = m.max(axis=0)                                   # [Hq]
+    Mu = np.where(np.isneginf(M), 0.0, M)
+    w = np.exp(m - Mu)                                  # [n, Hq]
+    den = (l * w).sum(axis=0)
+    num = (acc * w[:, :, None]).sum(axis=0)
+    if sink is not None:
+        z = np.asarray(sink, dtype=np.float64)
+        if sink_mode == "exp":
+            Mn = np.maximum(M, z)
+            f = np.exp(Mu - Mn)
+            den = den * f + np.exp(z - Mn)
+            num = num * f[:, None]
+        else:
+            den = den + z
+    with np.errstate(invalid="ignore", divide="ignore"):
+        return num / den[:, None]

@@ -1,0 +1,301 @@
+"""GPU parity of the HIP decode path against the CPU oracle.
+
+Inputs come from a CPU torch.Generator, so the oracle and the GPU see the same
+values.  Bars: fp16/bf16 outputs within atol = rtol = 2e-3 of the float64
+oracle plus half an ulp of the output dtype (the final cast's own rounding);
+fp8-KV outputs within atol = 1e-2; page gathers and the e4m3 decode table
+bit-exact.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from fasterkernels_amd import workloads as W
+from fasterkernels_amd.hip import decode as dec
+from oracle import decode_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def f64(t):
+    return t.detach().to(torch.float32).cpu().numpy().astype(np.float64)
+
+
+def half_ulp(ref, dtype):
+    mant = {torch.float16: 10, torch.bfloat16: 7, torch.float32: 23}[dtype]
+    emin = {torch.float16: -14, torch.bfloat16: -126, torch.float32: -126}[dtype]
+    e = np.floor(np.log2(np.maximum(np.abs(ref), 1e-30)))
+    return 0.5 * np.exp2(np.maximum(e, emin) - mant)
+
+
+def assert_close(out, ref, atol, rtol, what=""):
+    o = f64(out)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert o.shape == ref.shape, (o.shape, ref.shape)
+    tol = atol + rtol * np.abs(ref) + half_ulp(ref, out.dtype)
+    both_nan = np.isnan(o) & np.isnan(ref)
+    err = np.where(both_nan, 0.0, np.abs(o - ref))
+    bad = ~(err <= tol) & ~both_nan
+    if bad.any():
+        i = np.argwhere(bad)[0]
+        raise AssertionError(
+            f"{what}: {bad.sum()} / {bad.size} outside tolerance; first at {tuple(i)}: "
+            f"got {o[tuple(i)]!r}, want {ref[tuple(i)]!r}; max err/tol "
+            f"{np.nanmax(np.where(both_nan, 0, err / tol)):.3f}")
+
+
+def oracle_for(wl, sink_mode="exp"):
+    q = f64(wl.q)
+    s_aux = None if wl.s_aux is None else f64(wl.s_aux)
+    if wl.layout == "paged":
+        if wl.k_scale is not None:
+            kp = wl.k.view(torch.uint8).cpu().numpy()
+            vp = wl.v.view(torch.uint8).cpu().numpy()
+            return O.decode_paged(q, kp, vp, wl.block_table.cpu().numpy(), wl.lens, s_aux, sink_mode,
+                                  float(wl.k_scale), float(wl.v_scale))
+        return O.decode_paged(q, f64(wl.k), f64(wl.v), wl.block_table.cpu().numpy(), wl.lens, s_aux,
+                              sink_mode)
+    if wl.k_scale is not None:
+        k = O.dequantize_fp8(wl.k.view(torch.uint8).cpu().numpy(), float(wl.k_scale))
+        v = O.dequantize_fp8(wl.v.view(torch.uint8).cpu().numpy(), float(wl.v_scale))
+    else:
+        k, v = f64(wl.k), f64(wl.v)
+    return O.decode_varlen(q, k, v, wl.cu_seqlens.numpy(), s_aux, sink_mode)
+
+
+def tol_for(wl):
+    return (1e-2, 0.0) if wl.k.dtype == torch.float8_e4m3fn else (2e-3, 2e-3)
+
+
+def run_and_check(wl, sink_mode="exp", chunk_tokens=0, what=""):
+    ref = oracle_for(wl, sink_mode)
+    out = W.run(wl.to(DEV), sink_mode=sink_mode, chunk_tokens=chunk_tokens)
+    torch.cuda.synchronize()
+    atol, rtol = tol_for(wl)
+    assert_close(out, ref, atol, rtol, what or wl.name)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# bit-exact checks
+# ---------------------------------------------------------------------------
+def test_fp8_decode_table_bit_exact():
+    table = dec.fp8_decode_table(DEV).cpu()
+    codes = torch.arange(256, dtype=torch.uint8)
+    want = codes.view(torch.float8_e4m3fn).to(torch.float32)
+    for route in range(2):
+        got = table[route]
+        nan_w, nan_g = torch.isnan(want), torch.isnan(got)
+        assert torch.equal(nan_w, nan_g), f"route {route}: NaN codes differ"
+        assert torch.equal(got[~nan_g].view(torch.int32), want[~nan_w].view(torch.int32)), f"route {route}"
+    ora = O.e4m3_decode(np.arange(256, dtype=np.uint8))
+    assert np.array_equal(np.isnan(ora), torch.isnan(want).numpy())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float8_e4m3fn])
+def test_paged_gather_bit_exact(dtype):
+    kv = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float8_e4m3fn: "e4m3"}[dtype]
+    q = "bf16" if kv == "bf16" else "f16"
+    wl = W.make("C3", overrides=dict(B=5, lens=("list", [1, 16, 17, 250, 1000]), kv=kv, q=q), seed=7)
+    # poison everything past each sequence end in its last page
+    pool = wl.k.clone()
+    raw = pool.view(torch.uint8)
+    for b, L in enumerate(wl.lens):
+        if L % 16:
+            pg = int(wl.block_table[b, L // 16])
+            raw[pg, :, L % 16:, :] = 0x7F
+    got = dec.paged_gather(pool.to(DEV), wl.block_table.to(DEV), wl.seq_lens.to(DEV)).cpu()
+    want = O.paged_gather(raw.numpy(), wl.block_table.numpy(), wl.lens)
+    assert np.array_equal(got.view(torch.uint8).numpy(), want)
+
+
+# ---------------------------------------------------------------------------
+# paged
+# ---------------------------------------------------------------------------
+REF_LENS = [64, 512, 1024, 250]  # tests/test_triton_paged_gqa_decode.py:46
+
+
+@pytest.mark.parametrize("kv", ["f16", "bf16"])
+def test_paged_reference_case(kv):
+    wl = W.make("C3", overrides=dict(B=4, lens=("list", REF_LENS), kv=kv, q=kv, out=kv), seed=42)
+    run_and_check(wl, what=f"paged {kv}")
+
+
+@pytest.mark.parametrize("lens", [[1], [15], [16], [17], [31], [32], [33], [1, 2, 3, 4, 5, 6, 7],
+                                  [0, 5, 0, 40]])
+def test_paged_edge_lengths(lens):
+    wl = W.make("C3", overrides=dict(B=len(lens), lens=("list", lens)), seed=11)
+    if 0 in lens:
+        # zero-length rows: 0/0 without a sink, as in the reference kernels
+        out = W.run(wl.to(DEV))
+        torch.cuda.synchronize()
+        ref = oracle_for(wl)
+        assert_close(out, ref, 2e-3, 2e-3)
+        assert torch.isnan(out[[i for i, L in enumerate(lens) if L == 0]].float()).all()
+    else:
+        run_and_check(wl, what=f"lens {lens}")
+
+
+@pytest.mark.parametrize("chunk", [32, 64, 96, 128, 512])
+def test_paged_chunk_sizes(chunk):
+    wl = W.make("C3", overrides=dict(B=3, lens=("list", [33, 700, 2049])), seed=3)
+    run_and_check(wl, chunk_tokens=chunk, what=f"chunk {chunk}")
+
+
+@pytest.mark.parametrize("mode", ["exp", "linear"])
+@pytest.mark.parametrize("kv", ["f16", "bf16"])
+def test_paged_sinks(mode, kv):
+    wl = W.make("C3", overrides=dict(B=4, lens=("list", [1, 16, 300, 2000]), sinks=True, kv=kv, q=kv,
+                                     out=kv), seed=5)
+    run_and_check(wl, sink_mode=mode, what=f"sinks {mode} {kv}")
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 8), (32, 4), (64, 4), (32, 1), (48, 2)])
+def test_paged_group_sizes(Hq, Hkv):
+    wl = W.make("C3", overrides=dict(B=2, Hq=Hq, Hkv=Hkv, lens=("list", [77, 600])), seed=9)
+    run_and_check(wl, what=f"G={Hq // Hkv}")
+
+
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("kv", ["f16", "bf16", "e4m3"])
+def test_paged_head_dims(D, kv):
+    q = "bf16" if kv == "bf16" else "f16"
+    wl = W.make("C3", overrides=dict(B=2, D=D, lens=("list", [45, 530]), kv=kv, q=q, out=q), seed=13)
+    run_and_check(wl, what=f"D={D} {kv}")
+
+
+def test_paged_out_dtype_f32():
+    wl = W.make("C3", overrides=dict(B=2, lens=("list", [100, 1000]), out="f32"), seed=17)
+    run_and_check(wl, what="f32 out")
+
+
+def test_paged_fp8_c4_shape():
+    wl = W.make("C4", overrides=dict(lens=("list", [8192, 4000, 1, 777])))
+    run_and_check(wl, what="C4-like")
+
+
+@pytest.mark.parametrize("mode", ["exp", "linear"])
+def test_paged_fp8_sinks_skewed(mode):
+    wl = W.make("C5", overrides=dict(B=12), seed=21)
+    run_and_check(wl, sink_mode=mode, what=f"C5-like {mode}")
+
+
+def test_paged_fp16_q_fp8_kv():
+    wl = W.make("C4", overrides=dict(B=2, q="f16", out="f16", lens=("list", [3000, 50])), seed=23)
+    run_and_check(wl, what="f16 q + e4m3 kv")
+
+
+# ---------------------------------------------------------------------------
+# varlen
+# ---------------------------------------------------------------------------
+def test_varlen_c1():
+    run_and_check(W.make("C1"), what="C1")
+
+
+@pytest.mark.parametrize("mode", ["exp", "linear"])
+def test_varlen_reference_case(mode):
+    # tests/test_triton_fd_gqa.py:40-52 shapes: lens U[1024, 4096], 0.1*N(0,1) sinks
+    wl = W.make("C1", overrides=dict(lens=("uniform", 1024, 4096), sinks=True), seed=0)
+    wl.s_aux = wl.s_aux * 0.1
+    run_and_check(wl, sink_mode=mode, what=f"varlen ref {mode}")
+
+
+def test_varlen_zero_and_tiny():
+    wl = W.make("C1", overrides=dict(B=6, lens=("list", [0, 1, 2, 0, 33, 3]), sinks=True), seed=4)
+    run_and_check(wl, what="varlen tiny + sinks")
+
+
+def test_varlen_fp8():
+    wl = W.make("C1", overrides=dict(kv="e4m3", q="bf16", out="bf16"), seed=6)
+    run_and_check(wl, what="varlen fp8")
+
+
+# ---------------------------------------------------------------------------
+# dense (HF cache) and the fp8 reference API
+# ---------------------------------------------------------------------------
+def _dense_inputs(B, S, lens, starts, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, 32, 128, generator=g).to(dtype)
+    k = torch.randn(B, 8, S, 128, generator=g).to(dtype)
+    v = torch.randn(B, 8, S, 128, generator=g).to(dtype)
+    return q, k, v, torch.tensor(lens, dtype=torch.int32), (
+        None if starts is None else torch.tensor(starts, dtype=torch.int32))
+
+
+@pytest.mark.parametrize("num_splits", [None, 1, 8])
+def test_dense_hf(num_splits):
+    q, k, v, lens, starts = _dense_inputs(3, 1500, [1500, 700, 1], [0, 100, 0], torch.float16, 8)
+    out = dec.flash_decode_gqa_hf_dense_optimized(q.to(DEV), k.to(DEV), v.to(DEV), lens.to(DEV),
+                                                  starts.to(DEV), num_splits)
+    ref = O.decode_dense(f64(q), f64(k), f64(v), lens.numpy(), starts.numpy())
+    assert_close(out, ref, 2e-3, 2e-3, "dense")
+
+
+def test_hf_fp8_reference_api():
+    # tests/test_triton_gqa_decode_fp8.py:34-55 shapes: B=4, S=2048, lens U[512, 2048]
+    g = torch.Generator().manual_seed(42)
+    q = torch.randn(4, 32, 128, generator=g)
+    k = torch.randn(4, 8, 2048, 128, generator=g)
+    v = torch.randn(4, 8, 2048, 128, generator=g)
+    lens = torch.randint(512, 2049, (4,), generator=g, dtype=torch.int32)
+    q8, sq = dec.quantize_to_fp8(q)
+    k8, sk = dec.quantize_to_fp8(k)
+    v8, sv = dec.quantize_to_fp8(v)
+    for splits in (1, 8):
+        dec.set_num_splits_fp8(splits)
+        out = dec.flash_decode_gqa_hf_fp8(q8.to(DEV), k8.to(DEV), v8.to(DEV), lens.to(DEV), sq.to(DEV),
+                                          sk.to(DEV), sv.to(DEV), torch.float16)
+        # q is dequantised and rounded to fp16 by the reference before the dot
+        qd = (q8.to(torch.float32) * sq).to(torch.float16)
+        ref = O.decode_dense(f64(qd), k8.view(torch.uint8).numpy(), v8.view(torch.uint8).numpy(),
+                             lens.numpy(), k_scale=float(sk), v_scale=float(sv))
+        assert_close(out, ref, 1e-2, 0.0, f"hf fp8 splits={splits}")
+    dec.set_num_splits_fp8(1)
+
+
+# ---------------------------------------------------------------------------
+# properties at the headline size
+# ---------------------------------------------------------------------------
+def test_m0_full_size_parity_and_invariance():
+    wl = W.make("M0")
+    ref = oracle_for(wl)
+    g = wl.to(DEV)
+    out = W.run(g)
+    out_small_chunks = W.run(g, chunk_tokens=128)
+    torch.cuda.synchronize()
+    assert_close(out, ref, 2e-3, 2e-3, "M0")
+    assert_close(out_small_chunks, ref, 2e-3, 2e-3, "M0 chunk 128")
+    # batch permutation equivariance: permuting sequences permutes outputs exactly
+    perm = torch.tensor([2, 0, 3, 1])
+    out_p = dec.paged_flash_decode(g.q[perm.to(DEV)], g.k, g.v, g.block_table[perm.to(DEV)],
+                                   g.seq_lens[perm.to(DEV)], 16)
+    torch.cuda.synchronize()
+    assert torch.equal(out_p.cpu(), out.cpu()[perm])
+
+
+def test_c2_full_size_with_sinks():
+    run_and_check(W.make("C2"), what="C2")
+
+
+# ---------------------------------------------------------------------------
+# errors
+# ---------------------------------------------------------------------------
+def test_errors():
+    wl = W.make("C3", overrides=dict(B=2, lens=("list", [10, 20]))).to(DEV)
+    with pytest.raises(RuntimeError):
+        dec.paged_flash_decode(wl.q.cpu(), wl.k, wl.v, wl.block_table, wl.seq_lens, 16)
+    with pytest.raises(ValueError):
+        dec.paged_flash_decode(wl.q, wl.k, wl.v, wl.block_table, wl.seq_lens, 32)
+    with pytest.raises(ValueError):
+        W.run(wl, sink_mode="bogus")
+    q96 = torch.zeros(2, 32, 96, dtype=torch.float16, device=DEV)
+    k96 = torch.zeros(4, 8, 16, 96, dtype=torch.float16, device=DEV)
+    with pytest.raises(NotImplementedError):
+        dec.paged_flash_decode(q96, k96, k96, wl.block_table, wl.seq_lens, 16)
+    with pytest.raises(ValueError):  # fp8 pools need scales
+        k8 = wl.k.to(torch.float8_e4m3fn)
+        dec.paged_flash_decode(wl.q, k8, k8, wl.block_table, wl.seq_lens, 16)
