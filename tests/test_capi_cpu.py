@@ -1,0 +1,175 @@
+"""CPU checks of the C ABI: the library loads, exports exactly what
+include/fsk_decode.h declares, and rejects bad arguments on the host before
+any HIP call (so these run without a GPU)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from fasterkernels_amd import _native as nat
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "fsk_decode.h")
+FAKE = 0x10000  # 64 KiB-aligned dummy address; never dereferenced on the host
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"FSK_API\s+[\w\s\*]+?\b(fsk_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(nat.LIB_PATH):
+        from fasterkernels_amd import build
+        build.build()
+    return nat.load()
+
+
+def test_exports_match_header(lib):
+    declared = header_functions()
+    assert len(declared) >= 10
+    out = subprocess.run(["nm", "-D", "--defined-only", nat.LIB_PATH], capture_output=True, text=True).stdout
+    exported = sorted(set(re.findall(r"\bT (fsk_\w+)", out)))
+    assert exported == declared
+    assert sorted(nat.SIGNATURES) == declared
+    for name in declared:
+        assert getattr(lib, name) is not None
+
+
+def test_version_and_options(lib):
+    assert lib.fsk_version() == 1
+    assert lib.fsk_set_option(b"no_such_option", 1) == nat.FSK_ERR_INVALID
+    assert b"unknown option" in lib.fsk_last_error()
+    assert lib.fsk_set_option(b"chunk_tokens", 33) == nat.FSK_ERR_INVALID
+    assert lib.fsk_set_option(b"chunk_tokens", 0) == nat.FSK_OK
+    assert lib.fsk_set_option(b"waves_per_cu", 0) == nat.FSK_ERR_INVALID
+    assert lib.fsk_set_option(b"waves_per_cu", 8) == nat.FSK_OK
+
+
+def test_workspace_bytes(lib):
+    f = lib.fsk_workspace_bytes
+    a = f(nat.FSK_LAYOUT_PAGED, 4, 32, 8, 128, 2048, 16, 512)
+    b = f(nat.FSK_LAYOUT_PAGED, 4, 32, 8, 128, 2048, 16, 256)
+    assert 0 < a < b  # smaller splits -> more partials
+    # partial storage: units * Hkv * G * (D + 2) floats, plus the unit table
+    units = 4 * (2048 * 16 // 512)
+    assert a >= units * 8 * 4 * 130 * 4
+    assert f(nat.FSK_LAYOUT_VARLEN, 4, 32, 8, 128, 10000, 0, 0) > 0
+    assert f(nat.FSK_LAYOUT_DENSE, 4, 32, 8, 64, 4096, 0, 0) > 0
+    assert f(7, 4, 32, 8, 128, 2048, 16, 0) == nat.FSK_ERR_INVALID
+    assert f(nat.FSK_LAYOUT_PAGED, 4, 30, 8, 128, 2048, 16, 0) == nat.FSK_ERR_INVALID
+    assert f(nat.FSK_LAYOUT_PAGED, 4, 32, 8, 96, 2048, 16, 0) == nat.FSK_ERR_UNSUPPORTED
+    assert f(nat.FSK_LAYOUT_PAGED, 4, 32, 8, 128, 2048, 24, 0) == nat.FSK_ERR_UNSUPPORTED
+    assert f(nat.FSK_LAYOUT_PAGED, 4, 32, 8, 128, 2048, 16, 48) == nat.FSK_ERR_INVALID
+
+
+def paged_args(**kw):
+    """A valid argument set for fsk_decode_paged (fake pointers), overridable."""
+    a = dict(q=FAKE, q_sb=32 * 128, q_sh=128, k=FAKE, k_sp=8 * 16 * 128, k_sh=16 * 128, k_st=128,
+             v=FAKE, v_sp=8 * 16 * 128, v_sh=16 * 128, v_st=128, bt=FAKE, bt_sb=64, mb=64, lens=FAKE,
+             P=100, ps=16, sink=None, mode=0, ks=None, vs=None, out=FAKE, o_sb=32 * 128, o_sh=128,
+             B=4, Hq=32, Hkv=8, D=128, qdt=nat.FSK_F16, kvdt=nat.FSK_F16, odt=nat.FSK_F16,
+             scale=0.088, ws=FAKE, wsb=1 << 30, chunk=0, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("override,code", [
+    (dict(q=None), nat.FSK_ERR_INVALID),
+    (dict(lens=None), nat.FSK_ERR_INVALID),
+    (dict(bt=None), nat.FSK_ERR_INVALID),
+    (dict(Hq=30), nat.FSK_ERR_INVALID),
+    (dict(D=96), nat.FSK_ERR_UNSUPPORTED),
+    (dict(ps=24), nat.FSK_ERR_UNSUPPORTED),
+    (dict(mode=5), nat.FSK_ERR_INVALID),
+    (dict(odt=nat.FSK_E4M3), nat.FSK_ERR_UNSUPPORTED),
+    (dict(kvdt=nat.FSK_BF16), nat.FSK_ERR_UNSUPPORTED),        # q f16 with bf16 KV
+    (dict(kvdt=nat.FSK_E4M3), nat.FSK_ERR_INVALID),            # fp8 KV without scales
+    (dict(qdt=nat.FSK_E4M3, kvdt=nat.FSK_E4M3, ks=FAKE, vs=FAKE), nat.FSK_ERR_UNSUPPORTED),
+    (dict(k_st=100), nat.FSK_ERR_INVALID),                     # rows not 16-byte aligned
+    (dict(k_st=64), nat.FSK_ERR_INVALID),                      # overlapping rows
+    (dict(q=FAKE + 2), nat.FSK_ERR_INVALID),
+    (dict(bt_sb=10), nat.FSK_ERR_INVALID),                     # row stride < width
+    (dict(P=0), nat.FSK_ERR_INVALID),
+    (dict(ws=None), nat.FSK_ERR_WORKSPACE),
+    (dict(wsb=1024), nat.FSK_ERR_WORKSPACE),
+    (dict(chunk=48), nat.FSK_ERR_INVALID),
+    (dict(chunk=4096), nat.FSK_ERR_UNSUPPORTED),
+    (dict(scale=float("nan")), nat.FSK_ERR_INVALID),
+])
+def test_paged_validation(lib, override, code):
+    assert lib.fsk_decode_paged(*paged_args(**override)) == code
+    assert lib.fsk_last_error()  # a message explains the status
+
+
+def test_varlen_and_dense_validation(lib):
+    ok = [FAKE, 32 * 128, 128, FAKE, 8 * 128, 128, FAKE, 8 * 128, 128, FAKE, 1000, None, 0, None, None,
+          FAKE, 32 * 128, 128, 4, 32, 8, 128, nat.FSK_F16, nat.FSK_F16, nat.FSK_F16, 0.088, FAKE, 1 << 30, 0,
+          None]
+    bad = list(ok)
+    bad[21] = 80  # head_dim
+    assert lib.fsk_decode_varlen(*bad) == nat.FSK_ERR_UNSUPPORTED
+    bad = list(ok)
+    bad[9] = None  # cu_seqlens
+    assert lib.fsk_decode_varlen(*bad) == nat.FSK_ERR_INVALID
+    dense = [FAKE, 32 * 128, 128, FAKE, 8 * 512 * 128, 512 * 128, 128, FAKE, 8 * 512 * 128, 512 * 128, 128,
+             512, FAKE, None, None, 0, None, None, None, FAKE, 32 * 128, 128, 4, 32, 8, 128,
+             nat.FSK_E4M3, nat.FSK_E4M3, nat.FSK_F16, 0.088, FAKE, 1 << 30, 0, None]
+    assert lib.fsk_decode_dense(*dense) == nat.FSK_ERR_INVALID  # e4m3 KV without scales
+    assert b"scale" in lib.fsk_last_error()
+
+
+def test_debug_entry_validation(lib):
+    assert lib.fsk_fp8_decode_table(None, None) == nat.FSK_ERR_INVALID
+    assert lib.fsk_paged_gather(None, 0, 0, 0, FAKE, 4, 4, FAKE, 8, 16, 2, 8, 128, 0, FAKE, None) == nat.FSK_ERR_INVALID
+    assert lib.fsk_paged_gather(FAKE, 1, 1, 128, FAKE, 4, 4, FAKE, 8, 16, 2, 8, 128, 0, FAKE, None) == nat.FSK_ERR_INVALID
+    assert lib.fsk_paged_gather(FAKE, 8 * 16 * 128, 16 * 128, 128, FAKE, 4, 4, FAKE, 8, 16, 2, 8, 128,
+                                nat.FSK_F32, FAKE, None) == nat.FSK_ERR_UNSUPPORTED
+
+
+def test_timing_hook_without_gpu(lib):
+    a, b, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
+    assert lib.fsk_enable_kernel_timing(1) == nat.FSK_OK
+    assert lib.fsk_kernel_timing(ctypes.byref(a), ctypes.byref(b), ctypes.byref(n)) == nat.FSK_OK
+    assert n.value == 0
+    assert lib.fsk_enable_kernel_timing(0) == nat.FSK_OK
+    assert lib.fsk_kernel_timing(None, None, None) == nat.FSK_ERR_INVALID
+
+
+def test_python_wrappers_reject_host_tensors():
+    from fasterkernels_amd import paged_flash_decode, flash_decode_gqa_varlen
+    q = torch.zeros(2, 32, 128, dtype=torch.float16)
+    k = torch.zeros(4, 8, 16, 128, dtype=torch.float16)
+    bt = torch.zeros(2, 2, dtype=torch.int32)
+    with pytest.raises(RuntimeError):
+        paged_flash_decode(q, k, k, bt, torch.tensor([3, 4], dtype=torch.int32), 16)
+    with pytest.raises(RuntimeError):
+        flash_decode_gqa_varlen(q, k[0], k[0], torch.tensor([0, 1, 2], dtype=torch.int32))
+
+
+def test_fp8_kernels_keep_both_convert_halves():
+    """Regression guard for the compiler: every e4m3 widening in the decode
+    kernels must keep its high-word form (op_sel) next to the low-word one.
+    (A debug kernel that widened the converted values straight to fp32 lost
+    the high-word form in this compiler; the decode kernels must not.)"""
+    from fasterkernels_amd import build
+    res = subprocess.run([build.hipcc(), *[f for f in build.compile_flags() if f not in ("-shared", "-fPIC")],
+                          "--cuda-device-only", "-S", build.SRC, "-o", "-"],
+                         capture_output=True, text=True, timeout=600)
+    assert res.returncode == 0, res.stderr[-2000:]
+    asm = res.stdout
+    kernels = re.split(r"\n(?=_ZN12_GLOBAL__N_114partial_kernel)", asm)
+    checked = 0
+    for k in kernels[1:]:
+        name = k.split(":", 1)[0]
+        body = k.split("s_endpgm", 1)[0]
+        for ins in ("v_cvt_scalef32_pk_f16_fp8", "v_cvt_scalef32_pk_bf16_fp8"):
+            lo = len(re.findall(ins + r" v\d+, v\d+, 1\.0\s*$", body, re.M))
+            hi = len(re.findall(ins + r" .*op_sel", body))
+            assert lo == hi, f"{name}: {ins} low {lo} vs high {hi}"
+            checked += lo
+    assert checked > 0

@@ -1,0 +1,331 @@
+"""Pins the CPU oracle (oracle/decode_oracle.py) before it is trusted.
+
+Every oracle function is checked against something it does not share code
+with: torch's scaled_dot_product_attention and logsumexp (library routines),
+torch's float8_e4m3fn casts, the brute-force golden vectors in tests/golden/
+(pure-Python loops written from the definitions), closed forms and
+invariants.  The last test plants plausible mistakes in the oracle (wrong
+head mapping, dropped scale, swapped sink semantics, K/V swapped, transposed
+page addressing, off-by-one varlen slicing, dropped LSE weight) and requires
+that at least one pin fails for each.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import decode_oracle as O
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+rng = np.random.default_rng(1234)
+
+
+def sdpa(q, k, v, sink=None):
+    """torch SDPA reference for one sequence: q [Hq, D], k/v [L, Hkv, D].
+    An exp-mode sink is an extra key whose logit is the sink (additive mask)
+    and whose value is zero."""
+    Hq, D = q.shape
+    L, Hkv, _ = k.shape
+    G = Hq // Hkv
+    Q = torch.tensor(q)[:, None, :]                                    # [Hq, 1, D]
+    K = torch.tensor(k).permute(1, 0, 2).repeat_interleave(G, 0)       # [Hq, L, D]
+    V = torch.tensor(v).permute(1, 0, 2).repeat_interleave(G, 0)
+    mask = torch.zeros(Hq, 1, L, dtype=torch.float64)
+    if sink is not None:
+        K = torch.cat([K, torch.zeros(Hq, 1, D, dtype=K.dtype)], 1)
+        V = torch.cat([V, torch.zeros(Hq, 1, D, dtype=V.dtype)], 1)
+        mask = torch.cat([mask, torch.tensor(sink, dtype=torch.float64).view(Hq, 1, 1)], 2)
+    return F.scaled_dot_product_attention(Q, K, V, attn_mask=mask)[:, 0, :].numpy()
+
+
+def rand_case(Hq=8, Hkv=2, D=32, L=37):
+    return rng.standard_normal((Hq, D)), rng.standard_normal((L, Hkv, D)), rng.standard_normal((L, Hkv, D))
+
+
+# ---------------------------------------------------------------------------
+# pins, written as predicates so the planted-mistake test can reuse them
+# ---------------------------------------------------------------------------
+def pin_sdpa(ora):
+    for Hq, Hkv, D, L in [(8, 8, 16, 5), (8, 2, 32, 37), (32, 8, 128, 300), (6, 3, 64, 1)]:
+        q, k, v = rand_case(Hq, Hkv, D, L)
+        if not np.allclose(ora.attend(q, k, v), sdpa(q, k, v), atol=1e-12, rtol=1e-10):
+            return False
+    return True
+
+
+def pin_exp_sink(ora):
+    for L in (1, 9, 200):
+        q, k, v = rand_case(L=L)
+        z = rng.standard_normal(8) * 2
+        if not np.allclose(ora.attend(q, k, v, z, "exp"), sdpa(q, k, v, z), atol=1e-12, rtol=1e-10):
+            return False
+    return True
+
+
+def pin_linear_sink(ora):
+    """out_lin = out_plain * S / (S + z) with S = sum_t e^{s_t - max s} = e^{lse - max}."""
+    for L in (1, 9, 200):
+        q, k, v = rand_case(L=L)
+        z = np.abs(rng.standard_normal(8)) + 0.1
+        G = 4
+        s = torch.einsum("hd,lhd->hl", torch.tensor(q),
+                         torch.tensor(k).repeat_interleave(G, 1)) / math.sqrt(q.shape[1])
+        S = torch.exp(torch.logsumexp(s, 1) - s.max(1).values).numpy()
+        want = sdpa(q, k, v) * (S / (S + z))[:, None]
+        if not np.allclose(ora.attend(q, k, v, z, "linear"), want, atol=1e-12, rtol=1e-10):
+            return False
+    return True
+
+
+def pin_golden_varlen(ora):
+    g = np.load(os.path.join(GOLD, "varlen_small.npz"))
+    for mode, key in (("exp", "out_none"), ("exp", "out_exp"), ("linear", "out_linear")):
+        sink = None if key == "out_none" else g["s_aux"]
+        got = ora.decode_varlen(g["q"], g["k"], g["v"], g["cu_seqlens"], sink, mode)
+        if not np.allclose(got, g[key], atol=1e-12, rtol=1e-10):
+            return False
+    return True
+
+
+def pin_golden_paged(ora):
+    g = np.load(os.path.join(GOLD, "paged_small.npz"))
+    got = ora.decode_paged(g["q"], g["k_pool"], g["v_pool"], g["block_table"], g["seq_lens"])
+    if not np.allclose(got, g["out"], atol=1e-12, rtol=1e-10):
+        return False
+    f = np.load(os.path.join(GOLD, "paged_fp8_small.npz"))
+    got = ora.decode_paged(f["q"], f["k_codes"], f["v_codes"], f["block_table"], f["seq_lens"],
+                           f["s_aux"], "exp", float(f["k_scale"]), float(f["v_scale"]))
+    return bool(np.allclose(got, f["out"], atol=1e-10, rtol=1e-9))
+
+
+def pin_split_merge(ora):
+    for L in (1, 5, 64, 257):
+        q, k, v = rand_case(L=L)
+        z = rng.standard_normal(8)
+        full = ora.attend(q, k, v)
+        for n in (1, 2, 3, 8, L + 5):
+            acc, m, l = ora.partials(q, k, v, n)
+            if not np.allclose(ora.merge_partials(acc, m, l), full, atol=1e-12, rtol=1e-10):
+                return False
+            for mode in ("exp", "linear"):
+                zz = np.abs(z) if mode == "linear" else z
+                want = ora.attend(q, k, v, zz, mode)
+                if not np.allclose(ora.merge_partials(acc, m, l, zz, mode), want, atol=1e-12, rtol=1e-10):
+                    return False
+    return True
+
+
+def pin_closed_forms(ora):
+    q, k, v = rand_case(L=1)
+    if not np.allclose(ora.attend(q, k, v), np.repeat(v[0], 4, axis=0), atol=1e-14):
+        return False  # one token: the output is that token's value row
+    q, k, v = rand_case(L=23)
+    k[:] = k[:1]  # identical keys: uniform weights -> mean of the values
+    if not np.allclose(ora.attend(q, k, v), np.repeat(v.mean(0), 4, axis=0), atol=1e-12):
+        return False
+    q, k, v = rand_case(L=11)
+    if not np.allclose(ora.attend(q, k, v, np.full(8, -np.inf), "exp"), ora.attend(q, k, v), atol=1e-14):
+        return False
+    if not np.allclose(ora.attend(q, k, v, np.zeros(8), "linear"), ora.attend(q, k, v), atol=1e-14):
+        return False
+    # scores scale with sm_scale: doubling q equals doubling sm_scale
+    return bool(np.allclose(ora.attend(2 * q, k, v), ora.attend(q, k, v, sm_scale=2 / math.sqrt(32)), atol=1e-12))
+
+
+def pin_layouts(ora):
+    """Varlen, paged and dense entry points agree on the same logical sequences."""
+    Hq, Hkv, D = 8, 2, 16
+    lens = [3, 16, 33]
+    T = sum(lens)
+    q = rng.standard_normal((3, Hq, D))
+    k = rng.standard_normal((T, Hkv, D))
+    v = rng.standard_normal((T, Hkv, D))
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    ref = np.stack([ora.attend(q[b], k[cu[b]:cu[b + 1]], v[cu[b]:cu[b + 1]]) for b in range(3)])
+    if not np.allclose(ora.decode_varlen(q, k, v, cu), ref, atol=1e-13):
+        return False
+    # paged: build a shuffled pool like tests/test_triton_paged_gqa_decode.py:65-87
+    npg = [(L + 15) // 16 for L in lens]
+    P = sum(npg) + 3
+    perm = rng.permutation(P)
+    bt = -np.ones((3, max(npg)), dtype=np.int32)
+    kp = rng.standard_normal((P, Hkv, 16, D))
+    vp = rng.standard_normal((P, Hkv, 16, D))
+    o = 0
+    for b, L in enumerate(lens):
+        for j in range(npg[b]):
+            pg = perm[o]
+            o += 1
+            bt[b, j] = pg
+            n = min(16, L - 16 * j)
+            kp[pg, :, :n] = k[cu[b] + 16 * j: cu[b] + 16 * j + n].transpose(1, 0, 2)
+            vp[pg, :, :n] = v[cu[b] + 16 * j: cu[b] + 16 * j + n].transpose(1, 0, 2)
+    if not np.allclose(ora.decode_paged(q, kp, vp, bt, lens), ref, atol=1e-13):
+        return False
+    # dense with start offsets: pad each sequence behind 4 junk rows
+    S = max(lens) + 4
+    kd = rng.standard_normal((3, Hkv, S, D))
+    vd = rng.standard_normal((3, Hkv, S, D))
+    for b, L in enumerate(lens):
+        kd[b, :, 4:4 + L] = k[cu[b]:cu[b + 1]].transpose(1, 0, 2)
+        vd[b, :, 4:4 + L] = v[cu[b]:cu[b + 1]].transpose(1, 0, 2)
+    got = ora.decode_dense(q, kd, vd, np.array(lens) + 4, np.full(3, 4))
+    return bool(np.allclose(got, ref, atol=1e-13))
+
+
+def pin_gather(ora):
+    g = np.load(os.path.join(GOLD, "paged_small.npz"))
+    dense = ora.paged_gather(g["k_pool"], g["block_table"], g["seq_lens"])
+    for b, L in enumerate(g["seq_lens"]):
+        for t in range(dense.shape[2]):
+            want = g["k_pool"][g["block_table"][b, t // 16], :, t % 16] if t < L else 0.0
+            if not np.array_equal(dense[b, :, t], np.broadcast_to(want, dense[b, :, t].shape)):
+                return False
+    return True
+
+
+PINS = [pin_sdpa, pin_exp_sink, pin_linear_sink, pin_golden_varlen, pin_golden_paged,
+        pin_split_merge, pin_closed_forms, pin_layouts, pin_gather]
+
+
+@pytest.mark.parametrize("pin", PINS, ids=lambda f: f.__name__)
+def test_oracle_pinned(pin):
+    assert pin(O)
+
+
+# ---------------------------------------------------------------------------
+# e4m3 codec against torch's float8_e4m3fn and the golden table
+# ---------------------------------------------------------------------------
+def test_e4m3_decode_matches_torch_and_definition():
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn).to(torch.float32).numpy()
+    got = O.e4m3_decode(codes)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal(got[fin].view(np.int32), want[fin].view(np.int32))
+    gold = np.load(os.path.join(GOLD, "e4m3_table.npz"))["values"]
+    assert np.array_equal(np.isnan(gold), np.isnan(got))
+    assert np.array_equal(gold[fin], got[fin].astype(np.float64))
+
+
+def test_e4m3_encode_matches_torch_cast():
+    vals = np.concatenate([
+        rng.standard_normal(20000) * 50,
+        rng.standard_normal(5000) * 1e-2,        # subnormal range
+        O.e4m3_decode(np.arange(256, dtype=np.uint8)),
+        # exact midpoints between neighbouring codes (ties to even)
+        (O.e4m3_decode(np.arange(0, 126, dtype=np.uint8)).astype(np.float64)
+         + O.e4m3_decode(np.arange(1, 127, dtype=np.uint8))) / 2,
+        [0.0, -0.0, 448.0, -448.0, 449.0, 463.9, 1e-9, -1e-9, 2.0 ** -10, 3 * 2.0 ** -11],
+    ]).astype(np.float32)
+    vals = vals[~np.isnan(vals)]
+    want = torch.from_numpy(vals).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    got = O.e4m3_encode(vals)
+    bad = got != want
+    assert not bad.any(), (vals[bad][:5], got[bad][:5], want[bad][:5])
+
+
+def test_quantize_to_fp8_matches_reference_formula():
+    # restated formula: fskernels/triton/triton_gqa_decode_hf_fp8.py:13-16, via torch ops
+    for x in (rng.standard_normal((4, 8, 64)) * 3, np.zeros((3, 5)), rng.standard_normal(7) * 1e-20):
+        x = x.astype(np.float32)
+        t = torch.from_numpy(x)
+        scale = t.abs().max().clamp(min=1e-12) / 448.0
+        codes = (t / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        got_codes, got_scale = O.quantize_to_fp8(x)
+        assert np.float32(got_scale) == np.float32(scale.item())
+        assert np.array_equal(got_codes, codes)
+
+
+# ---------------------------------------------------------------------------
+# planted mistakes: every mutant must fail at least one pin
+# ---------------------------------------------------------------------------
+class Mutant:
+    """The oracle with one function replaced by a plausibly wrong variant."""
+
+    def __init__(self, **over):
+        self.__dict__.update({k: getattr(O, k) for k in dir(O) if not k.startswith("__")})
+        self.__dict__.update(over)
+
+
+def _attend_variant(kind):
+    def attend(q, k, v, sink=None, sink_mode="exp", sm_scale=None):
+        q = np.asarray(q, dtype=np.float64)
+        k = np.asarray(k, dtype=np.float64)
+        v = np.asarray(v, dtype=np.float64)
+        Hq, D = q.shape
+        L, Hkv, _ = k.shape
+        G = Hq // Hkv
+        scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
+        if kind == "noscale":
+            scale = 1.0
+        if kind == "kv_swap":
+            k, v = v, k
+        out = np.empty((Hq, D))
+        for h in range(Hq):
+            kv = h % Hkv if kind == "headmap" else h // G
+            s = k[:, kv, :] @ q[h] * scale
+            m = s.max() if L else -np.inf
+            mode = sink_mode
+            if kind == "sinkswap" and sink is not None:
+                mode = "linear" if sink_mode == "exp" else "exp"
+            if sink is not None and mode == "exp":
+                M = max(m, sink[h])
+                e = np.exp(s - M)
+                den = e.sum() + np.exp(sink[h] - M)
+            else:
+                e = np.exp(s - m)
+                den = e.sum() + (sink[h] if sink is not None else 0.0)
+            out[h] = e @ v[:, kv, :] / den
+        return out
+    return attend
+
+
+def _paged_rows_transposed(pool, block_table, b, length):
+    pool = np.asarray(pool)
+    ps = pool.shape[2]
+    t = np.arange(length)
+    return pool[np.asarray(block_table)[b, t % ps], :, t // ps, :]
+
+
+def _varlen_off_by_one(q, k, v, cu, s_aux=None, sink_mode="exp", sm_scale=None):
+    cu = np.asarray(cu)
+    return np.stack([O.attend(q[b], k[cu[b]:max(cu[b + 1] - 1, cu[b] + 1)], v[cu[b]:max(cu[b + 1] - 1, cu[b] + 1)],
+                              s_aux, sink_mode, sm_scale) for b in range(len(q))])
+
+
+def _merge_no_weight(acc, m, l, sink=None, sink_mode="exp"):
+    num = np.asarray(acc).sum(0)
+    den = np.asarray(l).sum(0)
+    return num / den[:, None]
+
+
+MUTANTS = {
+    "head mapping h % Hkv": Mutant(attend=_attend_variant("headmap")),
+    "sm_scale dropped": Mutant(attend=_attend_variant("noscale")),
+    "K and V swapped": Mutant(attend=_attend_variant("kv_swap")),
+    "sink semantics swapped": Mutant(attend=_attend_variant("sinkswap")),
+    "page index transposed": Mutant(paged_rows=_paged_rows_transposed),
+    "varlen off by one": Mutant(decode_varlen=_varlen_off_by_one),
+    "LSE weight dropped": Mutant(merge_partials=_merge_no_weight),
+}
+
+
+@pytest.mark.parametrize("name", list(MUTANTS))
+def test_planted_mistake_is_caught(name, monkeypatch):
+    mut = MUTANTS[name]
+    # functions that call each other inside the oracle module see the mutant too
+    for k, val in mut.__dict__.items():
+        if callable(val) and getattr(O, k, None) is not val:
+            monkeypatch.setattr(O, k, val)
+    def holds(pin):
+        try:
+            return pin(O)
+        except (IndexError, ValueError, FloatingPointError):
+            return False  # the mistake broke the oracle outright: caught
+
+    failed = [p.__name__ for p in PINS if not holds(p)]
+    assert failed, f"no pin caught the planted mistake: {name}"
