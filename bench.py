@@ -38,9 +38,34 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
-                                                      "profiles", "traffic_M0.json"),
-                    help="JSON with rocprof-derived HBM bytes per partial-kernel launch")
+                                                      "profiles", "partial_kernel_M0_traffic.md"),
+                    help="rocprof summary holding 'bytes_per_launch: N' for the partial kernel")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device copy of BYTES (counter calibration under rocprof)")
     return ap.parse_args()
+
+
+def copy_calibration(nbytes: int) -> None:
+    """A plain copy of known size: under rocprofv3 --pmc its FETCH_SIZE /
+    WRITE_SIZE per dispatch give the counters' scale factor."""
+    import torch
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes}), flush=True)
+
+
+def read_traffic(path: str):
+    """bytes_per_launch from a committed rocprof summary, or None."""
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.strip().startswith("bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def cpu_baseline(wl, budget_s: float):
@@ -104,6 +129,9 @@ def cpu_baseline(wl, budget_s: float):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only "
                                    "(see DESIGN.md), so --gpus must be 1", "n_gpus": args.gpus}))
@@ -131,7 +159,8 @@ def main():
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    nat.enable_kernel_timing(True)
+    # kernel durations: HIP events on one call in 8 of the timed region
+    nat.enable_kernel_timing(8)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -139,16 +168,13 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     part_ms, tot_ms, calls = nat.kernel_timing()
-    nat.enable_kernel_timing(False)
+    nat.enable_kernel_timing(0)
 
     ms_step = elapsed * 1e3 / args.steps
     gbs = alg_bytes / (ms_step / 1e3) / 1e9
     part_avg_ms = part_ms / max(calls, 1)
     kern_gbs = alg_bytes / (part_avg_ms / 1e3) / 1e9 if part_avg_ms > 0 else None
-    traffic = None
-    if os.path.exists(args.traffic) and args.config == "M0" and not args.chunk:
-        with open(args.traffic) as f:
-            traffic = json.load(f).get("bytes_per_launch")
+    traffic = read_traffic(args.traffic) if args.config == "M0" and not args.chunk else None
 
     out = {
         "metric": METRIC,

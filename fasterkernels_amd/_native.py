@@ -119,8 +119,9 @@ def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def enable_kernel_timing(enable: bool = True) -> None:
-    check(load().fsk_enable_kernel_timing(1 if enable else 0))
+def enable_kernel_timing(every_n: int = 1) -> None:
+    """Record HIP events around every n-th decode call (0 disables)."""
+    check(load().fsk_enable_kernel_timing(int(every_n)))
 
 
 def kernel_timing():

@@ -179,7 +179,8 @@ struct Params {
   const float* v_scale;
   float score_scale;       // sm_scale * log2(e)
   int B, Hkv, G, n_hb;
-  int chunk;               // tokens per unit (multiple of 32)
+  int chunk_min, chunk_max;  // split size bounds in tokens (multiples of 32)
+  int target_units;        // preferred number of sequence chunks per call
   int u_max;               // workspace capacity in units
   int32_t* plan;           // [B+1] unit prefix offsets
   float* part_ml;          // [u_max, Hkv, G, 2]
@@ -242,12 +243,36 @@ __device__ __forceinline__ HalfTile half_tile(const Params& p, int b, int start,
   return h;
 }
 
-// Builds the unit prefix table in LDS (pre[b] = first unit of sequence b,
-// pre[B] = total units, clamped to the workspace capacity) and returns the
-// total.  Workgroup 0 also publishes it for the reduce kernel.
+// Chooses the split size from the actual sequence lengths and builds the unit
+// prefix table in LDS (pre[b] = first unit of sequence b, pre[B] = total).
+// The split is the larger of
+//   * total_tokens / target_units (enough units to fill the GPU), and
+//   * total_tokens / (u_max - B) (so every unit fits the workspace),
+// clamped to [chunk_min, chunk_max]; the host sizes u_max for chunk_max, so
+// the table always fits.  Workgroup 0 publishes the table for the reduce
+// kernel.  Every workgroup computes the same result from the same lengths.
 template <int kLayout>
-__device__ int build_plan(const Params& p, int32_t* pre) {
+__device__ int build_plan(const Params& p, int32_t* pre, int& chunk_out) {
   const int lane = threadIdx.x;
+  int64_t total = 0;
+  for (int b0 = 0; b0 < p.B; b0 += kWave) {
+    int len = 0;
+    if (b0 + lane < p.B) {
+      int start;
+      seq_range<kLayout>(p, b0 + lane, start, len);
+    }
+    int sum = len;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+    total += sum;
+  }
+  int64_t want = (total + p.target_units - 1) / p.target_units;
+  if (p.u_max > p.B) want = std::max<int64_t>(want, (total + (p.u_max - p.B) - 1) / (p.u_max - p.B));
+  else want = p.chunk_max;
+  want = (want + 31) / 32 * 32;
+  const int chunk = uniform((int)std::min<int64_t>(std::max<int64_t>(want, p.chunk_min), p.chunk_max));
+  chunk_out = chunk;
+
   int carry = 0;
   for (int b0 = 0; b0 < p.B; b0 += kWave) {
     int b = b0 + lane;
@@ -255,7 +280,7 @@ __device__ int build_plan(const Params& p, int32_t* pre) {
     if (b < p.B) {
       int start, len;
       seq_range<kLayout>(p, b, start, len);
-      n = (len + p.chunk - 1) / p.chunk;
+      n = (len + chunk - 1) / chunk;
     }
     int incl = n;
 #pragma unroll
@@ -266,13 +291,13 @@ __device__ int build_plan(const Params& p, int32_t* pre) {
     if (b < p.B) pre[b] = min(carry + incl - n, p.u_max);
     carry += __shfl(incl, kWave - 1, kWave);
   }
-  const int total = min(carry, p.u_max);
-  if (lane == 0) pre[p.B] = total;
+  const int total_units = min(carry, p.u_max);
+  if (lane == 0) pre[p.B] = total_units;
   __syncthreads();
   if (blockIdx.x == 0) {
     for (int b = lane; b <= p.B; b += kWave) p.plan[b] = pre[b];
   }
-  return total;
+  return total_units;
 }
 
 // Largest b with pre[b] <= u (u < pre[B]).
@@ -497,15 +522,21 @@ __device__ __forceinline__ void compute_tile(const TileRegs<D, kKV>& T, Softmax<
   }
 }
 
+#ifndef FSK_PIPE_DEPTH
+#define FSK_PIPE_DEPTH 2
+#endif
+// Waves per SIMD the register budget is sized for (2: <= 256 VGPRs).
+constexpr int kWavesPerEu = FSK_PIPE_DEPTH > 2 ? 1 : 2;
+
 template <int D, int kQ, int kKV, int kLayout>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void partial_kernel(Params p) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu))) void partial_kernel(Params p) {
   using TR = TileRegs<D, kKV>;
   using SM = Softmax<D, kQ, kKV>;
   constexpr bool kKvFp8 = TR::kFp8;
   constexpr int kSteps = SM::kSteps;
   constexpr int kDpc = SM::kDpc;
-  // Two tiles of registers fit the 2-waves-per-SIMD budget up to D = 128.
-  constexpr bool kPipeline = (D <= 128);
+  // Tiles in flight per wave (registers: ~64 VGPRs per fp16 tile at D=128).
+  constexpr int kDepth = (D <= 128) ? FSK_PIPE_DEPTH : 1;
   static_assert(kKV != kBF16 || kQ == kBF16, "bf16 KV needs bf16 Q");
   static_assert(kKV != kF16 || kQ != kBF16, "f16 KV needs f16 Q");
 
@@ -514,7 +545,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
   const int g = lane >> 4;
   const int c = lane & 15;
 
-  const int total_units = build_plan<kLayout>(p, s_pre);
+  int chunk;
+  const int total_units = build_plan<kLayout>(p, s_pre, chunk);
   const int NH = p.Hkv * p.n_hb;
   const int64_t W = (int64_t)total_units * NH;
   const float k_scale = kKvFp8 ? p.k_scale[0] : 1.0f;
@@ -532,8 +564,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
     seq_range<kLayout>(p, un.b, un.start, un.len);
     un.start = uniform(un.start);
     un.len = uniform(un.len);
-    un.t_begin = cidx * p.chunk;
-    un.t_end = min(un.t_begin + p.chunk, un.len);
+    un.t_begin = cidx * chunk;
+    un.t_end = min(un.t_begin + chunk, un.len);
     un.p_first = 0;
     un.win0 = un.win1 = 0;
     if constexpr (kLayout == kPaged) {
@@ -581,19 +613,26 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
 #pragma unroll
     for (int j = 0; j < kDpc; ++j) st.acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    if constexpr (kPipeline) {
-      TR ta, tb;
+    if constexpr (kDepth > 1) {
+      // Tile slot s holds tile n with n % kDepth == s; while tile n is
+      // computed, tiles n+1 .. n+kDepth-1 are in flight.
+      TR tiles[kDepth];
       int t = un.t_begin;
-      issue_tile<D, kKV, kLayout>(ta, p, un, t, g, c);
-      while (true) {
-        if (t + 32 < un.t_end) issue_tile<D, kKV, kLayout>(tb, p, un, t + 32, g, c);
-        compute_tile<D, kQ, kKV>(ta, st, qop, sscale, g);
-        t += 32;
-        if (t >= un.t_end) break;
-        if (t + 32 < un.t_end) issue_tile<D, kKV, kLayout>(ta, p, un, t + 32, g, c);
-        compute_tile<D, kQ, kKV>(tb, st, qop, sscale, g);
-        t += 32;
-        if (t >= un.t_end) break;
+#pragma unroll
+      for (int s = 0; s < kDepth - 1; ++s)
+        if (t + 32 * s < un.t_end) issue_tile<D, kKV, kLayout>(tiles[s], p, un, t + 32 * s, g, c);
+      bool done = false;
+      while (!done) {
+#pragma unroll
+        for (int s = 0; s < kDepth; ++s) {
+          if (!done) {
+            const int tn = t + 32 * (kDepth - 1);
+            if (tn < un.t_end) issue_tile<D, kKV, kLayout>(tiles[(s + kDepth - 1) % kDepth], p, un, tn, g, c);
+            compute_tile<D, kQ, kKV>(tiles[s], st, qop, sscale, g);
+            t += 32;
+            done = t >= un.t_end;
+          }
+        }
       }
     } else {
       TR ta;
@@ -635,19 +674,23 @@ struct ReduceParams {
   int Hq, Hkv, G;
 };
 
-constexpr int kReduceWaves = 4;
+constexpr int kReduceThreads = 256;
 
 template <int D, int kOut>
-__global__ __launch_bounds__(64 * kReduceWaves) void reduce_kernel(ReduceParams p) {
-  // One workgroup per (query head, sequence); wave w merges units
-  // u0 + w, u0 + w + 4, ... and the waves combine through LDS.
-  constexpr int kE = D / kWave;  // output elements per lane
-  __shared__ float s_red[kReduceWaves];
-  __shared__ float s_num[kReduceWaves][D];
-  __shared__ float s_den[kReduceWaves];
+__global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) {
+  // One workgroup per (query head, sequence).  Thread t owns the float4
+  // column d4 = t % (D/4) of unit group grp = t / (D/4); group grp merges
+  // units grp, grp + kGroups, ... with an online LSE update, loading kPer
+  // units per round trip, and the groups combine through LDS.
+  constexpr int kD4 = D / 4;
+  constexpr int kGroups = kReduceThreads / kD4;
+  constexpr int kPer = 4;
+  __shared__ float s_m[kGroups];
+  __shared__ float s_l[kGroups];
+  __shared__ f32x4 s_acc[kGroups][kD4];
   const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wv = tid / kWave;
+  const int d4 = tid % kD4;
+  const int grp = tid / kD4;
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int kvh = h / p.G;
@@ -657,50 +700,55 @@ __global__ __launch_bounds__(64 * kReduceWaves) void reduce_kernel(ReduceParams 
   const int64_t base = ((int64_t)u0 * p.Hkv + kvh) * p.G + hg;  // partial index of unit u0
   const int64_t ustride = (int64_t)p.Hkv * p.G;                 // between consecutive units
 
-  float M = -INFINITY;
-  for (int i = tid; i < n; i += kWave * kReduceWaves) M = fmaxf(M, p.part_ml[2 * (base + i * ustride)]);
-  M = wave_max(M);
-  if (lane == 0) s_red[wv] = M;
-  __syncthreads();
-  M = s_red[0];
+  float m_t = -INFINITY, l_t = 0.f;
+  f32x4 a_t = {0.f, 0.f, 0.f, 0.f};
+  for (int i0 = grp; i0 < n; i0 += kGroups * kPer) {
+    f32x2 ml[kPer];
+    f32x4 ac[kPer];
 #pragma unroll
-  for (int w = 1; w < kReduceWaves; ++w) M = fmaxf(M, s_red[w]);
-  const float M_use = (M == -INFINITY) ? 0.f : M;
-
-  float den = 0.f;
-  float num[kE];
-#pragma unroll
-  for (int e = 0; e < kE; ++e) num[e] = 0.f;
-#pragma unroll 4
-  for (int i = wv; i < n; i += kReduceWaves) {
-    const int64_t idx = base + i * ustride;
-    const f32x2 ml = *(const f32x2*)(p.part_ml + 2 * idx);
-    const float* a = p.part_acc + idx * D + lane * kE;
-    float x[kE];
-    if constexpr (kE == 4) {
-      const f32x4 v = *(const f32x4*)a;
-      x[0] = v[0]; x[1] = v[1]; x[2] = v[2]; x[3] = v[3];
-    } else if constexpr (kE == 2) {
-      const f32x2 v = *(const f32x2*)a;
-      x[0] = v[0]; x[1] = v[1];
-    } else {
-      x[0] = a[0];
+    for (int j = 0; j < kPer; ++j) {
+      const int i = i0 + j * kGroups;
+      if (i < n) {
+        const int64_t idx = base + i * ustride;
+        ml[j] = *(const f32x2*)(p.part_ml + 2 * idx);
+        ac[j] = *(const f32x4*)(p.part_acc + idx * D + 4 * d4);
+      } else {
+        ml[j] = f32x2{-INFINITY, 0.f};
+        ac[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
     }
-    const float wgt = __builtin_amdgcn_exp2f(ml[0] - M_use);
-    den += ml[1] * wgt;
+    float mx = m_t;
 #pragma unroll
-    for (int e = 0; e < kE; ++e) num[e] += x[e] * wgt;
+    for (int j = 0; j < kPer; ++j) mx = fmaxf(mx, ml[j][0]);
+    const float mu = (mx == -INFINITY) ? 0.f : mx;
+    const float f = __builtin_amdgcn_exp2f(m_t - mu);
+    l_t *= f;
+    a_t *= f;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const float w = __builtin_amdgcn_exp2f(ml[j][0] - mu);
+      l_t += ml[j][1] * w;
+      a_t += ac[j] * w;
+    }
+    m_t = mx;
   }
-#pragma unroll
-  for (int e = 0; e < kE; ++e) s_num[wv][lane * kE + e] = num[e];
-  if (lane == 0) s_den[wv] = den;
+  if (d4 == 0) s_m[grp] = m_t;
   __syncthreads();
-  if (wv != 0) return;
+  float M = s_m[0];
 #pragma unroll
-  for (int w = 1; w < kReduceWaves; ++w) {
-    den += s_den[w];
+  for (int q = 1; q < kGroups; ++q) M = fmaxf(M, s_m[q]);
+  const float M_use = (M == -INFINITY) ? 0.f : M;
+  const float f = __builtin_amdgcn_exp2f(m_t - M_use);
+  s_acc[grp][d4] = a_t * f;
+  if (d4 == 0) s_l[grp] = l_t * f;
+  __syncthreads();
+  if (grp != 0) return;
+  f32x4 num = s_acc[0][d4];
+  float den = s_l[0];
 #pragma unroll
-    for (int e = 0; e < kE; ++e) num[e] += s_num[w][lane * kE + e];
+  for (int q = 1; q < kGroups; ++q) {
+    num += s_acc[q][d4];
+    den += s_l[q];
   }
 
   if (p.s_aux) {
@@ -710,23 +758,24 @@ __global__ __launch_bounds__(64 * kReduceWaves) void reduce_kernel(ReduceParams 
       const float z2 = z * kLog2e;
       const float Mn = fmaxf(M, z2);
       const float Mn_use = (Mn == -INFINITY) ? 0.f : Mn;
-      const float f = __builtin_amdgcn_exp2f(M_use - Mn_use);
-      den = den * f + __builtin_amdgcn_exp2f(z2 - Mn_use);
-#pragma unroll
-      for (int e = 0; e < kE; ++e) num[e] *= f;
+      const float fs = __builtin_amdgcn_exp2f(M_use - Mn_use);
+      den = den * fs + __builtin_amdgcn_exp2f(z2 - Mn_use);
+      num *= fs;
     } else {
       den += z;  // linear fold relative to the running max (flash_decode_cuda.cu:151-153)
     }
   }
 
   uint8_t* o = p.out + (int64_t)b * p.o_sb + (int64_t)h * p.o_sh;
-#pragma unroll
-  for (int e = 0; e < kE; ++e) {
-    const float val = num[e] / den;
-    const int d = lane * kE + e;
-    if constexpr (kOut == kF32) ((float*)o)[d] = val;
-    else if constexpr (kOut == kF16) ((f16*)o)[d] = (f16)val;
-    else ((bf16*)o)[d] = (bf16)val;
+  const f32x4 val = num / den;
+  if constexpr (kOut == kF32) {
+    *(f32x4*)((float*)o + 4 * d4) = val;
+  } else if constexpr (kOut == kF16) {
+    *(uint32_t __attribute__((ext_vector_type(2)))*)((f16*)o + 4 * d4) =
+        u32x2{pack_f16x2(val[0], val[1]), pack_f16x2(val[2], val[3])};
+  } else {
+    *(uint32_t __attribute__((ext_vector_type(2)))*)((bf16*)o + 4 * d4) =
+        u32x2{pack_bf16x2(val[0], val[1]), pack_bf16x2(val[2], val[3])};
   }
 }
 
@@ -778,16 +827,24 @@ int fail(int code, const std::string& msg) {
 }
 
 struct Options {
-  int chunk_tokens = 0;  // 0: automatic
-  int waves_per_cu = 8;
+  int chunk_tokens = 0;         // 0: automatic
+  int waves_per_cu = 8;         // persistent grid size (workgroups per CU)
+  int target_waves_per_cu = 4;  // automatic split: units of work per CU
 } g_opt;
 
 // Event triples recorded around decode calls while kernel timing is enabled.
 struct Timing {
   bool enabled = false;
-  std::vector<hipEvent_t> ev;  // 3 per call
+  int every = 1;       // record on every n-th decode call
+  int64_t calls = 0;
+  std::vector<hipEvent_t> ev;  // 3 per recorded call
   std::vector<hipEvent_t> spare;
 } g_timing;
+
+bool timing_this_call() {
+  if (!g_timing.enabled) return false;
+  return (g_timing.calls++ % g_timing.every) == 0;
+}
 
 hipEvent_t timing_event() {
   hipEvent_t e = nullptr;
@@ -800,8 +857,8 @@ hipEvent_t timing_event() {
   return e;
 }
 
-void timing_mark(hipStream_t s) {
-  if (!g_timing.enabled) return;
+void timing_mark(bool rec, hipStream_t s) {
+  if (!rec || !g_timing.enabled) return;
   hipEvent_t e = timing_event();
   if (e && hipEventRecord(e, s) == hipSuccess) g_timing.ev.push_back(e);
   else g_timing.enabled = false;  // could not record: stop timing rather than mis-pair
@@ -836,25 +893,42 @@ int device_cus() {
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
-// Split size: aim for about 8 units per CU-wave slot of work, clamped.
-int pick_chunk(int layout, int B, int Hkv, int n_hb, int64_t kv_extent, int page_size, int cus) {
-  if (g_opt.chunk_tokens > 0) return g_opt.chunk_tokens;
-  int64_t est_len;
-  if (layout == FSK_LAYOUT_VARLEN) est_len = cdiv(kv_extent, B);
-  else if (layout == FSK_LAYOUT_PAGED) est_len = kv_extent * page_size;
-  else est_len = kv_extent;
-  const int64_t rows = (int64_t)B * Hkv * n_hb * est_len;
-  int64_t ch = rows / ((int64_t)cus * g_opt.waves_per_cu);
-  ch = (ch + 31) / 32 * 32;
-  if (ch < 128) ch = 128;
-  if (ch > 2048) ch = 2048;
-  return (int)ch;
-}
+constexpr int kChunkMin = 128;   // smallest automatic split (tokens)
+constexpr int kChunkMax = 2048;  // largest split: 128 pages of 16 tokens per paged unit
 
+// Units a call can produce with split size `chunk` (host-side bound).
 int64_t unit_bound(int layout, int B, int64_t kv_extent, int page_size, int chunk) {
   if (layout == FSK_LAYOUT_VARLEN) return cdiv(kv_extent, chunk) + B;
   if (layout == FSK_LAYOUT_PAGED) return (int64_t)B * cdiv(kv_extent * page_size, chunk);
   return (int64_t)B * cdiv(kv_extent, chunk);
+}
+
+// Split policy of one call: a fixed split when the caller (or the
+// chunk_tokens option) asks for one, else bounds for the device-side choice
+// and a workspace capacity that always holds the chunk_max split.
+struct SplitPlan {
+  int chunk_min, chunk_max, target_units;
+  int64_t u_max;
+};
+SplitPlan plan_split(int layout, int B, int Hkv, int n_hb, int64_t kv_extent, int page_size, int chunk_tokens,
+                     int cus) {
+  SplitPlan sp;
+  const int fixed = chunk_tokens > 0 ? chunk_tokens : g_opt.chunk_tokens;
+  const int64_t nh = (int64_t)Hkv * n_hb;
+  if (fixed > 0) {
+    sp.chunk_min = sp.chunk_max = fixed;
+    sp.target_units = 1;
+    sp.u_max = unit_bound(layout, B, kv_extent, page_size, fixed);
+    return sp;
+  }
+  sp.chunk_min = kChunkMin;
+  sp.chunk_max = kChunkMax;
+  const int64_t target = std::max<int64_t>(1, (int64_t)cus * g_opt.target_waves_per_cu / nh);
+  sp.target_units = (int)std::min<int64_t>(target, 1 << 20);
+  const int64_t cap = std::max<int64_t>(4 * target, 256);
+  sp.u_max = std::max(unit_bound(layout, B, kv_extent, page_size, kChunkMax),
+                      std::min(unit_bound(layout, B, kv_extent, page_size, kChunkMin), cap));
+  return sp;
 }
 
 struct WsLayout {
@@ -958,7 +1032,7 @@ int dispatch_layout(int layout, const Params& p, int grid, int q_dt, int kv_dt, 
 template <int D>
 void launch_reduce(const ReduceParams& rp, int B, int o_dt, hipStream_t s) {
   dim3 grid(rp.Hq, B);
-  dim3 block(64 * kReduceWaves);
+  dim3 block(kReduceThreads);
   if (o_dt == FSK_F16) hipLaunchKernelGGL((reduce_kernel<D, kF16>), grid, block, 0, s, rp);
   else if (o_dt == FSK_BF16) hipLaunchKernelGGL((reduce_kernel<D, kBF16>), grid, block, 0, s, rp);
   else hipLaunchKernelGGL((reduce_kernel<D, kF32>), grid, block, 0, s, rp);
@@ -971,11 +1045,11 @@ int run_decode(const Common& c) {
   const int G = c.Hq / c.Hkv;
   const int n_hb = (G + 15) / 16;
   const int cus = device_cus();
-  int chunk = c.chunk > 0 ? c.chunk : pick_chunk(c.layout, c.B, c.Hkv, n_hb, c.kv_extent, c.page_size, cus);
-  if (chunk % 32 != 0 || chunk <= 0) return fail(FSK_ERR_INVALID, "chunk_tokens must be a positive multiple of 32");
-  if (c.layout == FSK_LAYOUT_PAGED && chunk > 2048)
+  if (c.chunk < 0 || c.chunk % 32 != 0) return fail(FSK_ERR_INVALID, "chunk_tokens must be 0 or a positive multiple of 32");
+  const SplitPlan sp = plan_split(c.layout, c.B, c.Hkv, n_hb, c.kv_extent, c.page_size, c.chunk, cus);
+  if (c.layout == FSK_LAYOUT_PAGED && sp.chunk_max > kChunkMax)
     return fail(FSK_ERR_UNSUPPORTED, "paged decode takes chunk_tokens <= 2048");
-  const int64_t u_max = unit_bound(c.layout, c.B, c.kv_extent, c.page_size, chunk);
+  const int64_t u_max = sp.u_max;
   if (u_max >= ((int64_t)1 << 31) / (c.Hkv * (int64_t)n_hb)) return fail(FSK_ERR_UNSUPPORTED, "too many work units");
   const WsLayout wl = ws_layout(c.B, c.Hkv, G, c.D, u_max);
   if (!c.ws || c.ws_bytes < wl.total || !aligned(c.ws, 256))
@@ -996,7 +1070,8 @@ int run_decode(const Common& c) {
   p.q_scale = c.q_scale; p.k_scale = c.k_scale; p.v_scale = c.v_scale;
   p.score_scale = c.sm_scale * kLog2e;
   p.B = c.B; p.Hkv = c.Hkv; p.G = G; p.n_hb = n_hb;
-  p.chunk = chunk; p.u_max = (int)u_max;
+  p.chunk_min = sp.chunk_min; p.chunk_max = sp.chunk_max; p.target_units = sp.target_units;
+  p.u_max = (int)u_max;
   uint8_t* ws = (uint8_t*)c.ws;
   p.plan = (int32_t*)(ws + wl.plan_off);
   p.part_ml = (float*)(ws + wl.ml_off);
@@ -1007,20 +1082,21 @@ int run_decode(const Common& c) {
   const int grid = (int)std::max<int64_t>(grid64, 1);
 
   (void)hipGetLastError();
-  timing_mark(c.stream);
+  const bool rec = timing_this_call();
+  timing_mark(rec, c.stream);
   int rc;
   if (c.D == 64) rc = dispatch_layout<64>(c.layout, p, grid, c.q_dt, c.kv_dt, c.stream);
   else if (c.D == 128) rc = dispatch_layout<128>(c.layout, p, grid, c.q_dt, c.kv_dt, c.stream);
   else rc = dispatch_layout<256>(c.layout, p, grid, c.q_dt, c.kv_dt, c.stream);
   if (rc != FSK_OK) {
-    if (g_timing.enabled && !g_timing.ev.empty()) {  // drop this call's first mark
+    if (rec && g_timing.enabled && !g_timing.ev.empty()) {  // drop this call's first mark
       g_timing.spare.push_back(g_timing.ev.back());
       g_timing.ev.pop_back();
     }
     return rc;
   }
 
-  timing_mark(c.stream);
+  timing_mark(rec, c.stream);
   ReduceParams rp;
   rp.plan = p.plan; rp.part_ml = p.part_ml; rp.part_acc = p.part_acc;
   rp.s_aux = c.s_aux; rp.sink_mode = c.sink_mode;
@@ -1029,7 +1105,7 @@ int run_decode(const Common& c) {
   if (c.D == 64) launch_reduce<64>(rp, c.B, c.o_dt, c.stream);
   else if (c.D == 128) launch_reduce<128>(rp, c.B, c.o_dt, c.stream);
   else launch_reduce<256>(rp, c.B, c.o_dt, c.stream);
-  timing_mark(c.stream);
+  timing_mark(rec, c.stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(FSK_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(e));
   return FSK_OK;
@@ -1058,12 +1134,20 @@ int fsk_set_option(const char* name, int64_t value) {
     g_opt.waves_per_cu = (int)value;
     return FSK_OK;
   }
+  if (!strcmp(name, "target_waves_per_cu")) {
+    if (value < 1 || value > 256) return fail(FSK_ERR_INVALID, "target_waves_per_cu in [1, 256]");
+    g_opt.target_waves_per_cu = (int)value;
+    return FSK_OK;
+  }
   return fail(FSK_ERR_INVALID, std::string("unknown option ") + name);
 }
 
-int fsk_enable_kernel_timing(int enable) {
+int fsk_enable_kernel_timing(int every_n) {
+  if (every_n < 0) return fail(FSK_ERR_INVALID, "every_n must be >= 0");
   timing_clear();
-  g_timing.enabled = enable != 0;
+  g_timing.enabled = every_n != 0;
+  g_timing.every = every_n > 0 ? every_n : 1;
+  g_timing.calls = 0;
   return FSK_OK;
 }
 
@@ -1105,9 +1189,8 @@ int64_t fsk_workspace_bytes(int layout, int batch, int num_q_heads, int num_kv_h
   const int G = num_q_heads / num_kv_heads;
   const int n_hb = (G + 15) / 16;
   const int B = batch > 0 ? batch : 1;
-  const int chunk = chunk_tokens > 0 ? chunk_tokens
-                                      : pick_chunk(layout, B, num_kv_heads, n_hb, kv_extent, page_size, device_cus());
-  const int64_t u_max = unit_bound(layout, B, kv_extent, page_size, chunk);
+  const SplitPlan sp = plan_split(layout, B, num_kv_heads, n_hb, kv_extent, page_size, chunk_tokens, device_cus());
+  const int64_t u_max = sp.u_max;
   return ws_layout(B, num_kv_heads, G, head_dim, u_max).total;
 }
 

@@ -167,18 +167,21 @@ FSK_API int fsk_paged_gather(const void *pool, int64_t stride_p, int64_t stride_
  * :90-92). */
 FSK_API int fsk_fp8_decode_table(uint16_t *out, void *stream);
 
-/* Tuning knobs for benchmarking sweeps ("chunk_tokens", "waves_per_cu").
+/* Tuning knobs for benchmarking sweeps:
+ *   "chunk_tokens"        fixed split size in tokens (0: chosen on the device)
+ *   "waves_per_cu"        persistent grid size, workgroups per CU (default 8)
+ *   "target_waves_per_cu" automatic split: units of work per CU (default 4)
  * Returns FSK_OK or FSK_ERR_INVALID for an unknown name or bad value. */
 FSK_API int fsk_set_option(const char *name, int64_t value);
 
 /* Profiling hook (no counterpart in the reference; used by the benchmark).
- * While enabled, every decode call records HIP events on its stream before the
- * split-KV partial kernel, between it and the reduce kernel, and after the
- * reduce kernel.  Not for use under HIP graph capture.  fsk_kernel_timing()
- * waits for the recorded events, returns the summed partial-kernel and
- * partial+reduce milliseconds and the number of decode calls, and clears the
- * record.  Disabling also clears it. */
-FSK_API int fsk_enable_kernel_timing(int enable);
+ * With every_n > 0, every n-th decode call records HIP events on its stream
+ * before the split-KV partial kernel, between it and the reduce kernel, and
+ * after the reduce kernel; every_n = 0 disables the hook.  Not for use under
+ * HIP graph capture.  fsk_kernel_timing() waits for the recorded events,
+ * returns the summed partial-kernel and partial+reduce milliseconds and the
+ * number of recorded calls, and clears the record. */
+FSK_API int fsk_enable_kernel_timing(int every_n);
 FSK_API int fsk_kernel_timing(double *partial_ms, double *total_ms, int64_t *calls);
 
 #ifdef __cplusplus
