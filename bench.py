@@ -149,8 +149,10 @@ def main():
     base = W.make(args.config, gen_device=dev, device=dev)
     kv_bytes = base.k.numel() * base.k.element_size() * 2
     n_sets = args.sets or max(1, min(8, -(-1_100_000_000 // kv_bytes)))
-    sets = [base] + [W.make(args.config, gen_device=dev, device=dev, seed=base.meta["seed"] + 1000 * i)
+    # same lengths and page tables, independent K/V data
+    sets = [base] + [W.make(args.config, gen_device=dev, device=dev, data_seed=base.meta["seed"] + 1000 * i)
                      for i in range(1, n_sets)]
+    assert all(s.lens == base.lens for s in sets)
     alg_bytes = base.algorithmic_bytes()
 
     def step(i):

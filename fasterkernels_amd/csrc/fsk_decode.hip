@@ -254,12 +254,22 @@ __device__ __forceinline__ HalfTile half_tile(const Params& p, int b, int start,
 template <int kLayout>
 __device__ int build_plan(const Params& p, int32_t* pre, int& chunk_out) {
   const int lane = threadIdx.x;
+  // Lengths of sequences lane, lane + 64, ...; the first block stays in a
+  // register so that the common case (B <= 64) reads them once.
+  int len0 = 0;
+  if (lane < p.B) {
+    int start;
+    seq_range<kLayout>(p, lane, start, len0);
+  }
   int64_t total = 0;
   for (int b0 = 0; b0 < p.B; b0 += kWave) {
-    int len = 0;
-    if (b0 + lane < p.B) {
-      int start;
-      seq_range<kLayout>(p, b0 + lane, start, len);
+    int len = len0;
+    if (b0 > 0) {
+      len = 0;
+      if (b0 + lane < p.B) {
+        int start;
+        seq_range<kLayout>(p, b0 + lane, start, len);
+      }
     }
     int sum = len;
 #pragma unroll
@@ -275,17 +285,20 @@ __device__ int build_plan(const Params& p, int32_t* pre, int& chunk_out) {
 
   int carry = 0;
   for (int b0 = 0; b0 < p.B; b0 += kWave) {
-    int b = b0 + lane;
-    int n = 0;
-    if (b < p.B) {
-      int start, len;
-      seq_range<kLayout>(p, b, start, len);
-      n = (len + chunk - 1) / chunk;
+    const int b = b0 + lane;
+    int len = len0;
+    if (b0 > 0) {
+      len = 0;
+      if (b < p.B) {
+        int start;
+        seq_range<kLayout>(p, b, start, len);
+      }
     }
+    const int n = (len + chunk - 1) / chunk;
     int incl = n;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) {
-      int y = __shfl_up(incl, off, kWave);
+      const int y = __shfl_up(incl, off, kWave);
       if (lane >= off) incl += y;
     }
     if (b < p.B) pre[b] = min(carry + incl - n, p.u_max);
@@ -758,7 +771,8 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) 
       const float z2 = z * kLog2e;
       const float Mn = fmaxf(M, z2);
       const float Mn_use = (Mn == -INFINITY) ? 0.f : Mn;
-      const float fs = __builtin_amdgcn_exp2f(M_use - Mn_use);
+      // An empty sequence (M = -inf, num = den = 0) keeps a zero numerator.
+      const float fs = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - Mn_use);
       den = den * fs + __builtin_amdgcn_exp2f(z2 - Mn_use);
       num *= fs;
     } else {

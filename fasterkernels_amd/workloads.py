@@ -129,18 +129,22 @@ def _quantize(x):
 
 
 def make(name: str = "M0", *, device=None, seed: int | None = None, overrides: dict | None = None,
-         gen_device=None) -> Workload:
+         gen_device=None, data_seed: int | None = None) -> Workload:
     """Builds a workload.  ``overrides`` replaces config keys (e.g. smaller
     ``B`` or ``lens`` for tests).  Random draws use a CPU generator unless
     ``gen_device`` names a GPU (faster for large benchmark inputs, different
-    values)."""
+    values).  ``data_seed`` redraws only Q/K/V/sinks: workloads made with the
+    same ``seed`` share lengths and page tables (rotating benchmark inputs)."""
     cfg = dict(CONFIGS[name])
     if overrides:
         cfg.update(overrides)
     seed = cfg["seed"] if seed is None else seed
     gdev = torch.device(gen_device) if gen_device is not None else torch.device("cpu")
     g = torch.Generator().manual_seed(seed)          # lengths, permutation (and data on CPU)
-    gd = g if gdev.type == "cpu" else torch.Generator(device=gdev).manual_seed(seed)
+    if data_seed is not None:
+        gd = torch.Generator(device=gdev).manual_seed(data_seed)
+    else:
+        gd = g if gdev.type == "cpu" else torch.Generator(device=gdev).manual_seed(seed)
     B, Hq, Hkv, D = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["D"]
     lens = _lengths(cfg["lens"], B, g)
     layout = cfg["layout"]

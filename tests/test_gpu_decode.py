@@ -299,3 +299,35 @@ def test_errors():
     with pytest.raises(ValueError):  # fp8 pools need scales
         k8 = wl.k.to(torch.float8_e4m3fn)
         dec.paged_flash_decode(wl.q, k8, k8, wl.block_table, wl.seq_lens, 16)
+
+
+# ---------------------------------------------------------------------------
+# graph capture
+# ---------------------------------------------------------------------------
+def test_hip_graph_replays_match_eager():
+    wl = W.make("C3", overrides=dict(B=5, lens=("list", [1, 40, 700, 3000, 9000]), sinks=True), seed=33).to(DEV)
+    other = W.make("C3", overrides=dict(B=2, lens=("list", [500, 17])), seed=34).to(DEV)
+    eager = W.run(wl).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):  # warm-up on the capture stream
+            W.run(wl)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        static_out = W.run(wl)
+    for i in range(4):
+        W.run(other)  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, eager), f"replay {i} differs from the eager result"
+
+
+def test_zero_length_with_very_negative_sink():
+    """An empty sequence with a sink far below zero: output 0, not NaN."""
+    wl = W.make("C1", overrides=dict(B=3, lens=("list", [0, 5, 0]), sinks=True), seed=35)
+    wl.s_aux = torch.full_like(wl.s_aux, -200.0)
+    run_and_check(wl, what="empty + sink -200")
