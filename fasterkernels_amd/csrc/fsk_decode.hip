@@ -54,6 +54,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Raw buffer resource dword 3 for gfx9-family parts (format fields unused by
 // raw dword loads).
 constexpr int kRsrcWord3 = 0x00020000;
+constexpr float E4M3_MAX_F = 448.f;  // largest finite e4m3fn value
 
 enum Layout { kVarlen = 0, kPaged = 1, kDense = 2 };
 enum Kind { kF16 = FSK_F16, kBF16 = FSK_BF16, kF32 = FSK_F32, kE4M3 = FSK_E4M3 };
@@ -831,6 +832,165 @@ __global__ __launch_bounds__(64) void fp8_table_kernel(uint32_t* out) {
 }
 
 // ---------------------------------------------------------------------------
+// KV write path: scatter new tokens' K/V rows into the page pools
+// ---------------------------------------------------------------------------
+// Token i of the batch goes to page slots[i] / page_size, row slots[i] %
+// page_size, of every KV head (fskernels/paged_attn/paged_kv_cache.py:117-130
+// does this per token with two indexed copies).  Each thread moves one
+// 8-element column group of one (token, head) row: consecutive threads cover a
+// row, then the next head, then the next token, so both the source read and
+// the pool write are contiguous 16-byte accesses (8 bytes for e4m3 pools).
+// Division by a divisor d fixed per launch, for dividends below 2^31:
+// q = (x * m) >> s with s = 31 + ceil(log2 d), m = ceil(2^s / d).  The error
+// term (m d - 2^s) x / (d 2^s) stays below 1/d, so q == x / d exactly.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+__device__ __forceinline__ uint32_t fdiv(uint32_t x, FastDiv f) {
+  return (uint32_t)(((uint64_t)x * f.m) >> f.s);
+}
+
+struct WriteParams {
+  const uint8_t* src[2];               // K, V: [n, Hkv, D] rows
+  int64_t s_st[2], s_sh[2];            // token / head strides, bytes
+  uint8_t* pool[2];                    // [P, Hkv, page_size, D]
+  int64_t p_sp[2], p_sh[2], p_st[2];   // page / head / row strides, bytes
+  const float* scale[2];               // e4m3 pools: quantisation scale, or null
+  const int64_t* slots;                // [n] page * page_size + row; < 0: skip
+  uint32_t n_slots;                    // num_pages * page_size (< 2^31)
+  uint32_t rows;                       // n * Hkv
+  FastDiv hkv, page;                   // divisors Hkv and page_size
+  int groups;                          // D / 8 column groups per row
+  int32_t* bt;                         // block-table updates: bt[upd[2j]] = upd[2j+1]
+  int64_t bt_numel;
+  const int64_t* upd;
+  int n_upd;
+};
+
+constexpr int kWriteThreads = 256;
+constexpr int kWriteUnroll = 4;
+
+template <int kSrc>
+__device__ __forceinline__ void load8(const uint8_t* p, float (&x)[8], u32x4& raw) {
+  if constexpr (kSrc == kF32) {
+    const f32x4 a = *(const f32x4*)p;
+    const f32x4 b = *(const f32x4*)(p + 16);
+    x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
+    x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
+  } else {
+    raw = *(const u32x4*)p;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // The element goes through a scalar: this compiler lowers
+      // __builtin_bit_cast of a vector-element operand to a load from the
+      // vector's first element.
+      const uint32_t w = raw[j];
+      if constexpr (kSrc == kF16) {
+        const f16x2 h = __builtin_bit_cast(f16x2, w);
+        x[2 * j] = (float)h[0];
+        x[2 * j + 1] = (float)h[1];
+      } else {
+        x[2 * j] = bf16_lo_to_f32(w);
+        x[2 * j + 1] = bf16_hi_to_f32(w);
+      }
+    }
+  }
+}
+
+// Four fp32 values -> four e4m3fn codes (round to nearest even, as torch's
+// float8_e4m3fn cast).  With a scale the values are first divided by it and
+// clamped to +-448 (the quantiser of
+// fskernels/triton/triton_gqa_decode_hf_fp8.py:13-16); without one they are
+// cast as they are, so magnitudes above 464 encode NaN as the cast does.  NaN
+// inputs give 0x7F with the input's sign bit, as the cast does.
+template <bool kScaled>
+__device__ __forceinline__ uint32_t encode_e4m3x4(const float* x, float s) {
+  float y[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    y[j] = x[j];
+    if constexpr (kScaled) y[j] = fminf(fmaxf(x[j] / s, -E4M3_MAX_F), E4M3_MAX_F);
+  }
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w, true);
+  uint32_t u = (uint32_t)w;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (x[j] != x[j]) {
+      const uint32_t code = 0x7Fu | ((f2u(x[j]) >> 31) << 7);
+      u = (u & ~(0xFFu << (8 * j))) | (code << (8 * j));
+    }
+  }
+  return u;
+}
+
+template <int kPool>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (kPool == kF16) return pack_f16x2(a, b);
+  else return pack_bf16x2(a, b);
+}
+
+template <int kSrc, int kPool, bool kScaled>
+__global__ __launch_bounds__(kWriteThreads) void kv_write_kernel(WriteParams p) {
+  const int kv = blockIdx.y;
+  if (blockIdx.x == 0 && kv == 0) {
+    for (int j = threadIdx.x; j < p.n_upd; j += kWriteThreads) {
+      const int64_t idx = p.upd[2 * j];
+      if (idx >= 0 && idx < p.bt_numel) p.bt[idx] = (int32_t)p.upd[2 * j + 1];
+    }
+  }
+  constexpr int kSrcBytes = (kSrc == kF32) ? 32 : 16;   // 8 source elements
+  constexpr int kDstBytes = (kPool == kE4M3) ? 8 : 16;  // 8 pool elements
+  // A block covers rows_per_block (token, head) rows per step, `groups`
+  // threads per row; the row stride between a thread's steps is fixed, so its
+  // column group never changes.
+  const uint32_t groups = p.groups;
+  const uint32_t rows_per_block = kWriteThreads / groups;
+  const uint32_t lrow = threadIdx.x / groups;
+  if (lrow >= rows_per_block) return;
+  const uint32_t g = threadIdx.x - lrow * groups;
+  const uint8_t* src = p.src[kv] + g * kSrcBytes;
+  uint8_t* pool = p.pool[kv] + g * kDstBytes;
+  const int64_t s_st = p.s_st[kv], s_sh = p.s_sh[kv];
+  const int64_t p_sp = p.p_sp[kv], p_sh = p.p_sh[kv], p_st = p.p_st[kv];
+  float scale = 1.f;
+  if constexpr (kScaled) scale = *p.scale[kv];
+  const uint32_t step = gridDim.x * rows_per_block;
+  for (uint32_t r0 = blockIdx.x * rows_per_block + lrow; r0 < p.rows; r0 += step * kWriteUnroll) {
+    float x[kWriteUnroll][8];
+    u32x4 raw[kWriteUnroll];
+    int64_t doff[kWriteUnroll];
+#pragma unroll
+    for (int u = 0; u < kWriteUnroll; ++u) {
+      doff[u] = -1;
+      const uint32_t row = r0 + u * step;
+      if (row >= p.rows) continue;
+      const uint32_t i = fdiv(row, p.hkv);
+      const uint32_t h = row - i * p.hkv.d;
+      const int64_t slot = p.slots[i];
+      if (slot < 0 || slot >= (int64_t)p.n_slots) continue;
+      const uint32_t page = fdiv((uint32_t)slot, p.page);
+      const uint32_t r = (uint32_t)slot - page * p.page.d;
+      load8<kSrc>(src + i * s_st + h * s_sh, x[u], raw[u]);
+      doff[u] = page * p_sp + h * p_sh + r * p_st;
+    }
+#pragma unroll
+    for (int u = 0; u < kWriteUnroll; ++u) {
+      if (doff[u] < 0) continue;
+      uint8_t* dst = pool + doff[u];
+      if constexpr (kPool == kE4M3) {
+        *(u32x2*)dst = u32x2{encode_e4m3x4<kScaled>(x[u], scale), encode_e4m3x4<kScaled>(x[u] + 4, scale)};
+      } else if constexpr (kPool == kSrc) {
+        *(u32x4*)dst = raw[u];  // same type: a bit-exact copy
+      } else {
+        *(u32x4*)dst = u32x4{pack2<kPool>(x[u][0], x[u][1]), pack2<kPool>(x[u][2], x[u][3]),
+                             pack2<kPool>(x[u][4], x[u][5]), pack2<kPool>(x[u][6], x[u][7])};
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 thread_local std::string g_err;
@@ -1125,6 +1285,97 @@ int run_decode(const Common& c) {
   return FSK_OK;
 }
 
+FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while (((uint64_t)1 << l) < d) ++l;
+  const uint64_t two_s = (uint64_t)1 << (31 + l);
+  return FastDiv{d, (uint32_t)((two_s + d - 1) / d), 31 + l};
+}
+
+template <int kSrc, int kPool, bool kScaled>
+void launch_write(const WriteParams& p, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((kv_write_kernel<kSrc, kPool, kScaled>), grid, dim3(kWriteThreads), 0, s, p);
+}
+
+template <int kSrc>
+void dispatch_write(const WriteParams& p, int pool_dt, bool scaled, dim3 grid, hipStream_t s) {
+  if (pool_dt == FSK_F16) launch_write<kSrc, kF16, false>(p, grid, s);
+  else if (pool_dt == FSK_BF16) launch_write<kSrc, kBF16, false>(p, grid, s);
+  else if (scaled) launch_write<kSrc, kE4M3, true>(p, grid, s);
+  else launch_write<kSrc, kE4M3, false>(p, grid, s);
+}
+
+struct WriteArgs {
+  const void* src[2]; int64_t s_st[2], s_sh[2];
+  const int64_t* slots; int64_t n;
+  void* pool[2]; int64_t p_sp[2], p_sh[2], p_st[2];
+  int num_pages, page_size, Hkv, D, src_dt, pool_dt;
+  const float* scale[2];
+  int32_t* bt; int64_t bt_numel; const int64_t* upd; int64_t n_upd;
+  hipStream_t stream;
+};
+
+int run_write(const WriteArgs& a) {
+  if (a.n < 0 || a.n_upd < 0) return fail(FSK_ERR_INVALID, "negative count");
+  if (a.Hkv <= 0 || a.D <= 0) return fail(FSK_ERR_INVALID, "num_kv_heads and head_dim must be positive");
+  if (a.D % 8 || a.D > 8 * kWriteThreads) return fail(FSK_ERR_UNSUPPORTED, "head_dim must be a multiple of 8, at most 2048");
+  if (a.page_size <= 0 || a.num_pages <= 0) return fail(FSK_ERR_INVALID, "page_size and num_pages must be positive");
+  if (a.src_dt != FSK_F16 && a.src_dt != FSK_BF16 && a.src_dt != FSK_F32)
+    return fail(FSK_ERR_UNSUPPORTED, "new K/V must be f16, bf16 or f32");
+  if (a.pool_dt != FSK_F16 && a.pool_dt != FSK_BF16 && a.pool_dt != FSK_E4M3)
+    return fail(FSK_ERR_UNSUPPORTED, "pools must be f16, bf16 or e4m3");
+  const bool scaled = a.scale[0] || a.scale[1];
+  if (scaled && (!a.scale[0] || !a.scale[1])) return fail(FSK_ERR_INVALID, "pass both k_scale and v_scale or neither");
+  if (scaled && a.pool_dt != FSK_E4M3) return fail(FSK_ERR_INVALID, "scales apply to e4m3 pools only");
+  if (a.n_upd > 0 && (!a.bt || !a.upd || a.bt_numel <= 0)) return fail(FSK_ERR_INVALID, "block-table updates need block_table");
+  if (a.n_upd >= (1 << 30)) return fail(FSK_ERR_UNSUPPORTED, "too many block-table updates");
+  const int se = elem_bytes(a.src_dt), pe = elem_bytes(a.pool_dt);
+  const int pa = pe == 1 ? 8 : 16;
+  for (int kv = 0; kv < 2; ++kv) {
+    if (a.n > 0 && (!a.src[kv] || !a.pool[kv])) return fail(FSK_ERR_INVALID, "null tensor pointer");
+    if (a.s_st[kv] < 0 || a.s_sh[kv] < 0 || a.p_sp[kv] < 0 || a.p_sh[kv] < 0 || a.p_st[kv] < 0)
+      return fail(FSK_ERR_INVALID, "negative stride");
+    if (!aligned(a.src[kv], 16) || (a.s_st[kv] * se) % 16 || (a.s_sh[kv] * se) % 16)
+      return fail(FSK_ERR_INVALID, "new K/V rows must be 16-byte aligned");
+    if (!aligned(a.pool[kv], pa) || (a.p_sp[kv] * pe) % pa || (a.p_sh[kv] * pe) % pa || (a.p_st[kv] * pe) % pa)
+      return fail(FSK_ERR_INVALID, "pool rows must be aligned to 8 elements' bytes");
+    if (a.page_size > 1 && a.p_st[kv] < a.D) return fail(FSK_ERR_INVALID, "pool row stride must be >= head_dim");
+  }
+  if (a.n && a.slots == nullptr) return fail(FSK_ERR_INVALID, "null slot_mapping");
+  const int64_t total = a.n * a.Hkv * (int64_t)(a.D / 8);
+  if (a.n >= ((int64_t)1 << 31) || total >= ((int64_t)1 << 31)) return fail(FSK_ERR_UNSUPPORTED, "batch too large for one call");
+  if ((int64_t)a.num_pages * a.page_size >= ((int64_t)1 << 31)) return fail(FSK_ERR_UNSUPPORTED, "pool above 2^31 slots");
+  if (total == 0 && a.n_upd == 0) return FSK_OK;
+
+  WriteParams p;
+  memset(&p, 0, sizeof(p));
+  for (int kv = 0; kv < 2; ++kv) {
+    p.src[kv] = (const uint8_t*)a.src[kv];
+    p.s_st[kv] = a.s_st[kv] * se; p.s_sh[kv] = a.s_sh[kv] * se;
+    p.pool[kv] = (uint8_t*)a.pool[kv];
+    p.p_sp[kv] = a.p_sp[kv] * pe; p.p_sh[kv] = a.p_sh[kv] * pe; p.p_st[kv] = a.p_st[kv] * pe;
+    p.scale[kv] = a.scale[kv];
+  }
+  p.slots = a.slots;
+  p.n_slots = (uint32_t)((int64_t)a.num_pages * a.page_size);
+  p.rows = (uint32_t)(a.n * a.Hkv);
+  p.hkv = make_fastdiv((uint32_t)a.Hkv);
+  p.page = make_fastdiv((uint32_t)a.page_size);
+  p.groups = a.D / 8;
+  p.bt = a.bt; p.bt_numel = a.bt_numel; p.upd = a.upd; p.n_upd = (int)a.n_upd;
+  const int64_t rows_per_block = kWriteThreads / p.groups;
+  const int64_t blocks = std::min<int64_t>(std::max<int64_t>(cdiv(p.rows, rows_per_block * kWriteUnroll), 1),
+                                           (int64_t)device_cus() * 8);
+  const dim3 grid((unsigned)blocks, 2);
+  (void)hipGetLastError();
+  if (a.src_dt == FSK_F16) dispatch_write<kF16>(p, a.pool_dt, scaled, grid, a.stream);
+  else if (a.src_dt == FSK_BF16) dispatch_write<kBF16>(p, a.pool_dt, scaled, grid, a.stream);
+  else dispatch_write<kF32>(p, a.pool_dt, scaled, grid, a.stream);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(FSK_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(e));
+  return FSK_OK;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -1324,6 +1575,27 @@ int fsk_fp8_decode_table(uint16_t* out, void* stream) {
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(FSK_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
   return FSK_OK;
+}
+
+int fsk_paged_write(const void* k_new, int64_t k_stride_t, int64_t k_stride_h, const void* v_new,
+                    int64_t v_stride_t, int64_t v_stride_h, const int64_t* slot_mapping, int64_t num_tokens,
+                    void* k_pool, int64_t k_stride_p, int64_t kp_stride_h, int64_t kp_stride_t, void* v_pool,
+                    int64_t v_stride_p, int64_t vp_stride_h, int64_t vp_stride_t, int num_pages, int page_size,
+                    int num_kv_heads, int head_dim, int src_dtype, int pool_dtype, const float* k_scale,
+                    const float* v_scale, int32_t* block_table, int64_t bt_numel, const int64_t* bt_updates,
+                    int64_t num_bt_updates, void* stream) {
+  WriteArgs a;
+  memset(&a, 0, sizeof(a));
+  a.src[0] = k_new; a.s_st[0] = k_stride_t; a.s_sh[0] = k_stride_h;
+  a.src[1] = v_new; a.s_st[1] = v_stride_t; a.s_sh[1] = v_stride_h;
+  a.slots = slot_mapping; a.n = num_tokens;
+  a.pool[0] = k_pool; a.p_sp[0] = k_stride_p; a.p_sh[0] = kp_stride_h; a.p_st[0] = kp_stride_t;
+  a.pool[1] = v_pool; a.p_sp[1] = v_stride_p; a.p_sh[1] = vp_stride_h; a.p_st[1] = vp_stride_t;
+  a.num_pages = num_pages; a.page_size = page_size; a.Hkv = num_kv_heads; a.D = head_dim;
+  a.src_dt = src_dtype; a.pool_dt = pool_dtype; a.scale[0] = k_scale; a.scale[1] = v_scale;
+  a.bt = block_table; a.bt_numel = bt_numel; a.upd = bt_updates; a.n_upd = num_bt_updates;
+  a.stream = (hipStream_t)stream;
+  return run_write(a);
 }
 
 }  // extern "C"

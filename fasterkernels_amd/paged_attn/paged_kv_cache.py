@@ -8,17 +8,24 @@ decode kernels' contract:
 
 A sequence's token ``pos`` lives in page ``block_table[seq, pos // PAGE_SIZE]``
 at row ``pos % PAGE_SIZE``; a page is taken from a LIFO free list when a
-sequence reaches a page boundary.  The host keeps a mirror of every
-sequence's page list, so no call reads the device block table back (the
-reference does, with ``.item()``, at :96 and :126); the resulting state is
-identical.
+sequence reaches a page boundary.
+
+Page bookkeeping stays on the host, as in the reference, with a host mirror of
+every sequence's page list, so no call reads the device block table back (the
+reference does, with ``.item()``, at :96 and :126).  The rows themselves are
+stored by the gfx950 write kernel: one launch per call stores every token of a
+batch and the new block-table entries together, so the pools must live on a
+HIP device.  e4m3 pools (``dtype=torch.float8_e4m3fn``) can carry per-tensor
+``k_scale``/``v_scale``; rows are then quantised on the way in.
 """
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import List
+from typing import List, Optional, Sequence, Tuple
 
 import torch
+
+from ..hip.kv_write import paged_kv_write
 
 PAGE_SIZE = 16  # tokens per physical page
 
@@ -37,6 +44,11 @@ class PagedKVCache:
                                  cache.get_block_table_tensor([sid]),
                                  cache.get_seq_lens_tensor([sid]), PAGE_SIZE)
         cache.free_sequence(sid)
+
+    Batched forms (no reference counterpart): ``append_kv_batch`` stores one
+    token for each of several sequences in one launch; ``reserve_slots`` +
+    ``write_kv`` take the slots of a step once and store every layer's rows
+    with one launch each.
     """
 
     num_layers: int
@@ -47,6 +59,8 @@ class PagedKVCache:
     head_dim: int
     dtype: torch.dtype
     device: str
+    k_scale: Optional[object] = None  # e4m3 pools: per-tensor scale (float or fp32 tensor)
+    v_scale: Optional[object] = None
 
     def __post_init__(self):
         # One pool per layer for K and for V (paged_kv_cache.py:46-50).
@@ -61,6 +75,13 @@ class PagedKVCache:
         self._active: List[bool] = [False] * self.max_seqs
         self._free_pages: List[int] = list(range(self.num_pages))
         self._pages: List[List[int]] = [[] for _ in range(self.max_seqs)]
+        if (self.k_scale is None) != (self.v_scale is None):
+            raise ValueError("give both k_scale and v_scale or neither")
+        if self.k_scale is not None:
+            if self.dtype != torch.float8_e4m3fn:
+                raise ValueError("k_scale/v_scale apply to float8_e4m3fn pools only")
+            self.k_scale = torch.as_tensor(self.k_scale, dtype=torch.float32).reshape(()).to(self.k_pool.device)
+            self.v_scale = torch.as_tensor(self.v_scale, dtype=torch.float32).reshape(()).to(self.k_pool.device)
 
     @classmethod
     def from_config(cls, config, num_pages: int = 4096, max_seqs: int = 16,
@@ -102,6 +123,65 @@ class PagedKVCache:
         return self._free_pages.pop()
 
     # ------------------------------------------------------------------
+    def _plan(self, seq_ids: Sequence[int], num_tokens: int = 1) -> Tuple[List[int], List[Tuple[int, int]]]:
+        """Host bookkeeping of appending ``num_tokens`` tokens to each listed
+        sequence, in list order (a repeated id appends again, as repeated
+        append_kv calls would).  Returns the slots (page * PAGE_SIZE + row,
+        sequence-major) and the block-table stores (flat index, page).  All or
+        nothing: a call that would run out of pages or past a block-table row
+        raises before any state changes."""
+        lens = {}
+        need = 0
+        for sid in seq_ids:
+            pos = lens.get(sid, self._seq_lens[sid])
+            end = pos + num_tokens
+            if -(-end // PAGE_SIZE) > self.max_blocks_per_seq:
+                raise IndexError(f"sequence {sid} would need more than max_blocks_per_seq="
+                                 f"{self.max_blocks_per_seq} pages")
+            need += -(-end // PAGE_SIZE) - -(-pos // PAGE_SIZE)
+            lens[sid] = end
+        if need > len(self._free_pages):
+            raise RuntimeError("Out of KV pages")
+        row_stride = self.block_table.stride(0)
+        slots: List[int] = []
+        updates: List[Tuple[int, int]] = []
+        for sid in seq_ids:
+            pages = self._pages[sid]
+            pos = self._seq_lens[sid]
+            for _ in range(num_tokens):
+                lp, off = divmod(pos, PAGE_SIZE)
+                if off == 0:
+                    pp = self._alloc_page()
+                    pages.append(pp)
+                    updates.append((sid * row_stride + lp, pp))
+                else:
+                    pp = pages[lp]
+                slots.append(pp * PAGE_SIZE + off)
+                pos += 1
+            self._seq_lens[sid] = pos
+        return slots, updates
+
+    def _require_gpu(self):
+        if not self.k_pool.is_cuda:
+            raise RuntimeError("PagedKVCache stores rows with the HIP write kernel; "
+                               f"its pools are on {self.k_pool.device}, not a GPU")
+
+    def _stage(self, slots, updates):
+        """One host->device copy of the slots and block-table stores."""
+        vals = list(slots)
+        for flat, page in updates:
+            vals += (flat, page)
+        host = torch.tensor(vals, dtype=torch.int64, pin_memory=True)
+        dev = host.to(self.k_pool.device, non_blocking=True)
+        n = len(slots)
+        return dev[:n], dev[n:].view(-1, 2)
+
+    def _write(self, layer_idx, k, v, slot_dev, upd_dev):
+        paged_kv_write(k, v, self.k_pool[layer_idx], self.v_pool[layer_idx], slot_dev,
+                       k_scale=self.k_scale, v_scale=self.v_scale,
+                       block_table=self.block_table, bt_updates=upd_dev)
+
+    # ------------------------------------------------------------------
     def append_kv(self, seq_id: int, layer_idx: int, k: torch.Tensor, v: torch.Tensor):
         """Appends one token's K/V ([1, Hkv, 1, D]) to a sequence (:109-132).
 
@@ -109,18 +189,38 @@ class PagedKVCache:
         sequence length advances on every call, so callers append each layer
         of a token through the same page bookkeeping.
         """
-        pos = self._seq_lens[seq_id]
-        page_idx = pos // PAGE_SIZE
-        page_offset = pos % PAGE_SIZE
-        if page_offset == 0:
-            pp = self._alloc_page()
-            self.block_table[seq_id, page_idx] = pp
-            self._pages[seq_id].append(pp)
-        else:
-            pp = self._pages[seq_id][page_idx]
-        self.k_pool[layer_idx, pp, :, page_offset, :] = k[0, :, 0, :]
-        self.v_pool[layer_idx, pp, :, page_offset, :] = v[0, :, 0, :]
-        self._seq_lens[seq_id] = pos + 1
+        self.append_kv_batch([seq_id], layer_idx, k, v)
+
+    def append_kv_batch(self, seq_ids: Sequence[int], layer_idx: int, k: torch.Tensor, v: torch.Tensor):
+        """append_kv for several tokens in one launch: token j of k/v
+        ([n, Hkv, 1, D] or [n, Hkv, D]) goes to sequence seq_ids[j]; the
+        bookkeeping is that of n append_kv calls in order."""
+        self._require_gpu()
+        if k.shape[0] != len(seq_ids) or v.shape[0] != len(seq_ids):
+            raise ValueError(f"k/v hold {k.shape[0]}/{v.shape[0]} tokens for {len(seq_ids)} sequences")
+        slots, updates = self._plan(list(seq_ids), 1)
+        slot_dev, upd_dev = self._stage(slots, updates)
+        self._write(layer_idx, k, v, slot_dev, upd_dev)
+
+    def reserve_slots(self, seq_ids: Sequence[int], num_tokens: int = 1) -> torch.Tensor:
+        """Takes ``num_tokens`` new positions in each listed sequence (pages as
+        needed, block table stored on the device) and returns their slots, an
+        int64 device tensor [len(seq_ids) * num_tokens], sequence-major, for
+        ``write_kv`` of every layer."""
+        self._require_gpu()
+        slots, updates = self._plan(list(seq_ids), int(num_tokens))
+        slot_dev, upd_dev = self._stage(slots, updates)
+        if updates:
+            empty = self.k_pool.new_empty((0, self.num_kv_heads, self.head_dim), dtype=torch.float32)
+            self._write(0, empty, empty, slot_dev[:0], upd_dev)
+        return slot_dev
+
+    def write_kv(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor):
+        """Stores rows k/v ([n, Hkv, D], any strides with a contiguous head_dim,
+        or [n, Hkv, 1, D]) of one layer at slots from ``reserve_slots``."""
+        self._require_gpu()
+        paged_kv_write(k, v, self.k_pool[layer_idx], self.v_pool[layer_idx], slot_mapping,
+                       k_scale=self.k_scale, v_scale=self.v_scale)
 
     # ------------------------------------------------------------------
     def get_block_table_tensor(self, active_seq_ids: List[int]) -> torch.Tensor:

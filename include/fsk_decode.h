@@ -148,6 +148,41 @@ FSK_API int fsk_decode_dense(const void *q, int64_t q_stride_b, int64_t q_stride
                      void *workspace, int64_t workspace_bytes, int chunk_tokens,
                      void *stream);
 
+/* KV write path: store a batch of new tokens' K/V into the page pools.
+ * Replaces: fskernels/paged_attn/paged_kv_cache.py:109-132 (PagedKVCache.append_kv:
+ *           block-table store :122-124 and the two indexed row copies :129-130),
+ *           batched over tokens and fused into one launch.
+ * k_new/v_new [n, Hkv, D] (token stride, head stride; head_dim contiguous,
+ * 16-byte aligned rows) in f16, bf16 or f32.  slot_mapping int64 [n]: token i
+ * is written to page slot_mapping[i] / page_size, row slot_mapping[i] %
+ * page_size, of every head; a negative slot or one >= num_pages * page_size
+ * skips the token.  Pools [P, Hkv, page_size, D] in f16, bf16 or e4m3:
+ *   - f16/bf16 pools: the source is copied (same dtype: bit-exact) or cast
+ *     with round-to-nearest-even;
+ *   - e4m3 pools with k_scale/v_scale (device fp32 scalars, finite and > 0):
+ *     code = e4m3(clamp(x / scale, -448, 448)), the quantiser of
+ *     fskernels/triton/triton_gqa_decode_hf_fp8.py:13-16 with a fixed scale;
+ *   - e4m3 pools without scales: a plain e4m3fn cast (|x| > 464 -> NaN).
+ *   NaN inputs encode as 0x7F | sign, like torch's float8_e4m3fn cast.
+ * Optionally the same launch stores block-table entries:
+ * block_table[bt_updates[2j]] = (int32)bt_updates[2j+1] for j < num_bt_updates
+ * (flat element indices; indices outside [0, bt_numel) are skipped).  The
+ * writes are ordered before later work on `stream`; tokens that share a slot
+ * race. */
+FSK_API int fsk_paged_write(const void *k_new, int64_t k_stride_t, int64_t k_stride_h,
+                    const void *v_new, int64_t v_stride_t, int64_t v_stride_h,
+                    const int64_t *slot_mapping, int64_t num_tokens,
+                    void *k_pool, int64_t k_stride_p, int64_t k_stride_h_pool,
+                    int64_t k_stride_t_pool,
+                    void *v_pool, int64_t v_stride_p, int64_t v_stride_h_pool,
+                    int64_t v_stride_t_pool,
+                    int num_pages, int page_size, int num_kv_heads, int head_dim,
+                    int src_dtype, int pool_dtype,
+                    const float *k_scale, const float *v_scale,
+                    int32_t *block_table, int64_t bt_numel,
+                    const int64_t *bt_updates, int64_t num_bt_updates,
+                    void *stream);
+
 /* Debug: gather a paged pool into a dense [B, Hkv, max_blocks*page_size, D]
  * tensor through the decode kernels' own page-addressing routine; rows at or
  * past seq_lens[b] are written as zero.  Bit-exact copy of the element bytes.

@@ -27,6 +27,11 @@ It restates, in plain numpy, what the reference computes on the decode path:
   k[b, h, :, :] (fskernels/triton/triton_gqa_decode_hf.py:46-54, :62-64).
 * Split-KV partials and their log-sum-exp merge
   (triton_gqa_decode_hf.py:52-54, :90-99, :103-137).
+* The KV write path: PagedKVCache's page bookkeeping and row stores
+  (fskernels/paged_attn/paged_kv_cache.py:44-141) restated as
+  RefPagedKVCache, and the slot-addressed batch store paged_write with the
+  element encodings a pool can hold (f16 / bf16 round to nearest even, e4m3
+  plain cast or fixed-scale quantisation).
 * e4m3fn (OCP FP8, torch.float8_e4m3fn) decoding from the format definition,
   encoding with round-to-nearest-even, and the per-tensor quantiser
   scale = max|x|.clamp(1e-12) / 448, x8 = e4m3(clamp(x / scale, +-448))
@@ -70,8 +75,9 @@ def e4m3_encode(x) -> np.ndarray:
     """float -> uint8 code, round to nearest (ties to even code), NaN -> 0x7F.
 
     Magnitudes above 448 are not clamped here (the quantiser clamps first,
-    triton_gqa_decode_hf_fp8.py:15); they round to 448 if below the 464
-    midpoint, else encode NaN as torch's float8_e4m3fn cast does.
+    triton_gqa_decode_hf_fp8.py:15); they round to 448 up to the 464 midpoint
+    (the tie goes to the even code 448), beyond it they encode NaN, as torch's
+    float8_e4m3fn cast does.
     """
     x = np.asarray(x, dtype=np.float64)
     a = np.abs(x)
@@ -82,7 +88,7 @@ def e4m3_encode(x) -> np.ndarray:
     pick_hi = (a - lo > hi - a) | ((a - lo == hi - a) & ((idx % 2) == 0))
     code = np.where(pick_hi, idx, idx - 1)
     code = np.where(a <= _E4M3_POS[0], 0, code)
-    code = np.where(a >= 464.0, 0x7F, code)  # past the last midpoint: NaN
+    code = np.where(a > 464.0, 0x7F, code)  # past the last midpoint (464 ties to 448): NaN
     code = np.where(np.isnan(a), 0x7F, code)
     sign = np.where(np.signbit(x), 0x80, 0)
     return (code | sign).astype(np.uint8)
@@ -260,3 +266,128 @@ def merge_partials(acc, m, l, sink=None, sink_mode="exp"):
             den = den + z
     with np.errstate(invalid="ignore", divide="ignore"):
         return num / den[:, None]
+
+
+# ---------------------------------------------------------------------------
+# KV write path
+# ---------------------------------------------------------------------------
+def bf16_bits(x) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns (uint16), round to nearest, ties to even.
+
+    NaN maps to 0x7FC0 here; the write kernels keep NaN a NaN but its payload
+    is not pinned."""
+    x = np.asarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(np.isnan(x), np.uint16(0x7FC0), r)
+
+
+def bf16_to_f32(bits) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def encode_kv(x, pool_dtype: str, scale=None) -> np.ndarray:
+    """Pool elements for float32 values x.
+
+    'f16'  -> float16, round to nearest even (numpy's conversion);
+    'bf16' -> uint16 bfloat16 bits (bf16_bits);
+    'e4m3' -> uint8 codes: with a scale, e4m3(clamp(x / scale, -448, 448)) in
+              fp32 -- the quantiser of triton_gqa_decode_hf_fp8.py:13-16 with a
+              fixed scale; without one, the plain e4m3fn cast that a torch copy
+              into an e4m3 pool performs (paged_kv_cache.py:129-130).
+    """
+    x = np.asarray(x, dtype=np.float32)
+    if pool_dtype == "f16":
+        with np.errstate(over="ignore"):
+            return x.astype(np.float16)
+    if pool_dtype == "bf16":
+        return bf16_bits(x)
+    if pool_dtype == "e4m3":
+        if scale is not None:
+            with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+                x = np.clip(x / np.float32(scale), -E4M3_MAX, E4M3_MAX).astype(np.float32)
+        return e4m3_encode(x)
+    raise ValueError(f"unknown pool dtype {pool_dtype!r}")
+
+
+def paged_store_rows(pool, slots, rows):
+    """Stores row i of rows [n, Hkv, D] (already in the pool's element type) at
+    page slots[i] // ps, row slots[i] % ps of every head of pool [P, Hkv, ps, D]
+    (in place, returned).  Slots outside [0, P * ps) are skipped.  Restates the
+    per-token row store of paged_kv_cache.py:117-130 for a batch of slots; a
+    store between equal element types is this byte copy."""
+    P, Hkv, ps, D = pool.shape
+    rows = np.asarray(rows).reshape(-1, Hkv, D)
+    for i, s in enumerate(np.asarray(slots, dtype=np.int64).reshape(-1)):
+        if 0 <= s < P * ps:
+            pool[s // ps, :, s % ps, :] = rows[i]
+    return pool
+
+
+def paged_write(pool, slots, x, pool_dtype: str, scale=None):
+    """paged_store_rows of float32 values x [n, Hkv, D] encoded for the pool."""
+    Hkv, D = pool.shape[1], pool.shape[3]
+    enc = encode_kv(np.asarray(x, dtype=np.float32).reshape(-1, Hkv, D), pool_dtype, scale)
+    return paged_store_rows(pool, slots, enc)
+
+
+_POOL_NP = {"f16": np.float16, "bf16": np.uint16, "e4m3": np.uint8}
+
+
+class RefPagedKVCache:
+    """Restatement of fskernels/paged_attn/paged_kv_cache.py:44-141 in numpy.
+
+    Pools [L, P, Hkv, 16, D] hold encoded elements (encode_kv), zero-filled
+    (:46-50); block_table [max_seqs, max_blocks] int32 starts at -1 (:53-56);
+    the free list starts as [0, 1, ..., P-1] and pages are popped from its end
+    (:61, :103-106); allocate_sequence takes the lowest inactive slot (:85-91);
+    free_sequence returns a sequence's pages in logical order (:93-101);
+    append_kv stores token pos at page block_table[s, pos // 16], row pos % 16,
+    taking a new page when pos % 16 == 0, and advances the length (:109-132).
+    """
+
+    page_size = 16
+
+    def __init__(self, num_layers, num_pages, max_seqs, max_blocks, num_kv_heads, head_dim,
+                 pool_dtype="f16", k_scale=None, v_scale=None):
+        shape = (num_layers, num_pages, num_kv_heads, self.page_size, head_dim)
+        self.k_pool = np.zeros(shape, dtype=_POOL_NP[pool_dtype])
+        self.v_pool = np.zeros(shape, dtype=_POOL_NP[pool_dtype])
+        self.block_table = np.full((max_seqs, max_blocks), -1, dtype=np.int32)
+        self.seq_lens = [0] * max_seqs
+        self.active = [False] * max_seqs
+        self.free_pages = list(range(num_pages))
+        self.pool_dtype, self.k_scale, self.v_scale = pool_dtype, k_scale, v_scale
+
+    def allocate_sequence(self) -> int:
+        for sid, on in enumerate(self.active):
+            if not on:
+                self.active[sid] = True
+                self.seq_lens[sid] = 0
+                return sid
+        raise RuntimeError("All sequence slots are occupied")
+
+    def free_sequence(self, sid: int) -> None:
+        n_pages = -(-self.seq_lens[sid] // self.page_size)
+        for lp in range(n_pages):
+            pp = int(self.block_table[sid, lp])
+            if pp >= 0:
+                self.free_pages.append(pp)
+                self.block_table[sid, lp] = -1
+        self.active[sid] = False
+        self.seq_lens[sid] = 0
+
+    def append_kv(self, sid: int, layer: int, k, v) -> None:
+        """k, v: [Hkv, D] float32 values of one token."""
+        pos = self.seq_lens[sid]
+        lp, off = divmod(pos, self.page_size)
+        if off == 0:
+            if not self.free_pages:
+                raise RuntimeError("Out of KV pages")
+            pp = self.free_pages.pop()
+            self.block_table[sid, lp] = pp
+        else:
+            pp = int(self.block_table[sid, lp])
+        self.k_pool[layer, pp, :, off, :] = encode_kv(k, self.pool_dtype, self.k_scale)
+        self.v_pool[layer, pp, :, off, :] = encode_kv(v, self.pool_dtype, self.v_scale)
+        self.seq_lens[sid] = pos + 1

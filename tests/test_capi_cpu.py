@@ -131,6 +131,76 @@ def test_debug_entry_validation(lib):
                                 nat.FSK_F32, FAKE, None) == nat.FSK_ERR_UNSUPPORTED
 
 
+def write_args(**kw):
+    """A valid argument set for fsk_paged_write (fake pointers), overridable."""
+    a = dict(k=FAKE, k_st=8 * 128, k_sh=128, v=FAKE, v_st=8 * 128, v_sh=128, slots=FAKE, n=4,
+             kp=FAKE, kp_sp=8 * 16 * 128, kp_sh=16 * 128, kp_st=128, vp=FAKE, vp_sp=8 * 16 * 128,
+             vp_sh=16 * 128, vp_st=128, P=100, ps=16, Hkv=8, D=128, sdt=nat.FSK_F16, pdt=nat.FSK_F16,
+             ks=None, vs=None, bt=None, bt_numel=0, upd=None, n_upd=0, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("override,code", [
+    (dict(k=None), nat.FSK_ERR_INVALID),
+    (dict(slots=None), nat.FSK_ERR_INVALID),
+    (dict(n=-1), nat.FSK_ERR_INVALID),
+    (dict(Hkv=0), nat.FSK_ERR_INVALID),
+    (dict(D=100), nat.FSK_ERR_UNSUPPORTED),                    # not a multiple of 8
+    (dict(D=4096), nat.FSK_ERR_UNSUPPORTED),
+    (dict(ps=0), nat.FSK_ERR_INVALID),
+    (dict(P=0), nat.FSK_ERR_INVALID),
+    (dict(sdt=nat.FSK_E4M3), nat.FSK_ERR_UNSUPPORTED),         # source must be f16/bf16/f32
+    (dict(pdt=nat.FSK_F32), nat.FSK_ERR_UNSUPPORTED),
+    (dict(ks=FAKE), nat.FSK_ERR_INVALID),                      # one scale only
+    (dict(ks=FAKE, vs=FAKE), nat.FSK_ERR_INVALID),             # scales on an f16 pool
+    (dict(k=FAKE + 8), nat.FSK_ERR_INVALID),                   # unaligned source rows
+    (dict(k_st=100), nat.FSK_ERR_INVALID),
+    (dict(kp_st=100), nat.FSK_ERR_INVALID),
+    (dict(kp_st=64), nat.FSK_ERR_INVALID),                     # overlapping pool rows
+    (dict(kp_sh=-16), nat.FSK_ERR_INVALID),
+    (dict(n_upd=2, upd=FAKE), nat.FSK_ERR_INVALID),            # updates without a block table
+    (dict(P=1 << 28, ps=16), nat.FSK_ERR_UNSUPPORTED),         # 2^32 slots
+])
+def test_paged_write_validation(lib, override, code):
+    assert lib.fsk_paged_write(*write_args(**override)) == code
+    assert lib.fsk_last_error()
+
+
+def test_paged_write_noop_without_gpu(lib):
+    # nothing to store and nothing to update: returns before any HIP call
+    assert lib.fsk_paged_write(*write_args(n=0, k=None, v=None, kp=None, vp=None, slots=None)) == nat.FSK_OK
+
+
+def test_no_bit_cast_of_vector_elements():
+    """This hipcc lowers __builtin_bit_cast(T, vec[i]) to a load of the
+    vector's first element; the sources must go through a scalar instead."""
+    from fasterkernels_amd import build
+    src = open(build.SRC).read()
+    bad = re.findall(r"__builtin_bit_cast\(\s*\w+\s*,\s*\w+\s*\[[^]]*\]\s*\)", src)
+    assert not bad, bad
+
+
+def test_write_kernels_load_whole_source_groups():
+    """Every column group of the KV write kernels loads 16 bytes of an f16 /
+    bf16 source (32 of f32) and widens all eight elements."""
+    from fasterkernels_amd import build
+    res = subprocess.run([build.hipcc(), *[f for f in build.compile_flags() if f not in ("-shared", "-fPIC")],
+                          "--cuda-device-only", "-S", build.SRC, "-o", "-"],
+                         capture_output=True, text=True, timeout=600)
+    assert res.returncode == 0, res.stderr[-2000:]
+    found = 0
+    for m in re.finditer(r"\n(_ZN12_GLOBAL__N_115kv_write_kernelILi(\d)ELi(\d)ELb(\d)\w*):[^\n]*\n(.*?)s_endpgm",
+                         res.stdout, re.S):
+        src_dt, pool_dt, body = int(m.group(2)), int(m.group(3)), m.group(5)
+        x4 = len(re.findall(r"global_load_dwordx4", body))
+        assert x4 == (8 if src_dt == nat.FSK_F32 else 4), (m.group(1), x4)   # 4 rows per thread
+        if src_dt == nat.FSK_F16 and pool_dt != nat.FSK_F16:
+            assert len(re.findall(r"v_cvt_f32_f16", body)) == 32, m.group(1)
+        found += 1
+    assert found == 12
+
+
 def test_timing_hook_without_gpu(lib):
     a, b, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
     assert lib.fsk_enable_kernel_timing(1) == nat.FSK_OK

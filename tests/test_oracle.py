@@ -6,8 +6,9 @@ torch's float8_e4m3fn casts, the brute-force golden vectors in tests/golden/
 (pure-Python loops written from the definitions), closed forms and
 invariants.  The last test plants plausible mistakes in the oracle (wrong
 head mapping, dropped scale, swapped sink semantics, K/V swapped, transposed
-page addressing, off-by-one varlen slicing, dropped LSE weight) and requires
-that at least one pin fails for each.
+page addressing, off-by-one varlen slicing, dropped LSE weight, transposed
+write slots, truncating bf16, a wrong e4m3 tie, a quantiser without clamp, a
+FIFO free list) and requires that at least one pin fails for each.
 """
 import math
 import os
@@ -187,8 +188,102 @@ def pin_gather(ora):
     return True
 
 
+def _encode_values():
+    """Values that exercise every rounding and range rule of the pool encodings."""
+    u = rng.integers(0, 1 << 15, 4000).astype(np.uint32)
+    bf16_ties = ((u << 16) | 0x8000).view(np.float32)           # halfway between bf16 neighbours
+    h = rng.integers(0, 0x7C00, 4000).astype(np.uint16)
+    f16_ties = (h.view(np.float16).astype(np.float32).view(np.uint32) | 0x1000).view(np.float32)
+    codes = np.arange(0, 127, dtype=np.uint8)
+    e4m3_mid = (O.e4m3_decode(codes[:-1]).astype(np.float64) + O.e4m3_decode(codes[1:])) / 2
+    special = [0.0, -0.0, 448.0, -448.0, 449.0, 463.99, 464.0, -464.0, 464.01, 470.0, 480.0, 1e6, -1e6,
+               np.inf, -np.inf, 65504.0, 65520.0, 1e-8, -1e-8, 2.0 ** -24, 2.0 ** -25, 3e38, -3e38]
+    v = np.concatenate([rng.standard_normal(20000) * 40, rng.standard_normal(4000) * 1e-3,
+                        bf16_ties, -bf16_ties, f16_ties, -f16_ties, e4m3_mid, -e4m3_mid, special])
+    with np.errstate(over="ignore", invalid="ignore"):
+        v = v.astype(np.float32)
+    return v[~np.isnan(v)]
+
+
+def pin_kv_encode(ora):
+    """Pool encodings against torch's casts (library routines) of the same fp32 values."""
+    x = _encode_values()
+    t = torch.from_numpy(x)
+    if not np.array_equal(ora.encode_kv(x, "f16").view(np.uint16), t.to(torch.float16).view(torch.int16).numpy().view(np.uint16)):
+        return False
+    if not np.array_equal(ora.encode_kv(x, "bf16"), t.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)):
+        return False
+    xn = np.concatenate([x, np.array([np.nan, -np.nan], dtype=np.float32)])
+    tn = torch.from_numpy(xn)
+    if not np.array_equal(ora.encode_kv(xn, "e4m3"), tn.to(torch.float8_e4m3fn).view(torch.uint8).numpy()):
+        return False
+    for scale in (np.float32(0.0123), np.float32(2.5), np.float32(1.0)):
+        want = (tn / torch.tensor(scale)).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        if not np.array_equal(ora.encode_kv(xn, "e4m3", scale), want):
+            return False
+    return True
+
+
+def pin_paged_write(ora):
+    """Rows written through block-table slots read back through paged_rows
+    (pinned above on the golden gather) as the encoded rows; other rows stay."""
+    P, Hkv, ps, D = 9, 3, 16, 8
+    for dt in ("f16", "bf16", "e4m3"):
+        pool = np.full((P, Hkv, ps, D), 7, dtype=ora._POOL_NP[dt])
+        bt = rng.permutation(P)[:4].reshape(2, 2)
+        lens = [21, 32]
+        x = [rng.standard_normal((L, Hkv, D)).astype(np.float32) for L in lens]
+        for b, L in enumerate(lens):
+            t = np.arange(L)
+            slots = bt[b, t // ps] * ps + t % ps
+            ora.paged_write(pool, slots, x[b], dt, 0.01 if dt == "e4m3" else None)
+            if not np.array_equal(ora.paged_rows(pool, bt, b, L), ora.encode_kv(x[b], dt, 0.01 if dt == "e4m3" else None)):
+                return False
+        # a skipped slot and an out-of-range slot leave the pool alone
+        before = pool.copy()
+        ora.paged_write(pool, [-1, P * ps], np.zeros((2, Hkv, D), np.float32), dt)
+        if not np.array_equal(pool, before):
+            return False
+        # rows past sequence 0's length in its last page keep the fill value
+        if not (pool[bt[0, 1], :, 21 - ps:, :] == 7).all():
+            return False
+    return True
+
+
+def pin_ref_cache(ora):
+    """Page bookkeeping facts of fskernels/paged_attn/paged_kv_cache.py: lowest
+    free slot (:85-91), pages popped from the end of [0..P-1] (:61, :106),
+    freed pages appended in logical order (:93-101), a new page at each
+    16-token boundary (:122-124), "Out of KV pages" (:104-105)."""
+    c = ora.RefPagedKVCache(1, 8, 3, 4, 2, 8, "f16")
+    if [c.allocate_sequence() for _ in range(3)] != [0, 1, 2]:
+        return False
+    for pos in range(33):
+        c.append_kv(0, 0, np.full((2, 8), pos + 1.0, np.float32), np.full((2, 8), -(pos + 1.0), np.float32))
+    if c.block_table[0].tolist() != [7, 6, 5, -1] or c.seq_lens[0] != 33:
+        return False
+    if not (c.k_pool[0, 6, :, 1, :] == 18.0).all() or not (c.v_pool[0, 5, :, 0, :] == -33.0).all():
+        return False
+    c.free_sequence(0)
+    if c.free_pages != [0, 1, 2, 3, 4, 7, 6, 5] or c.allocate_sequence() != 0:
+        return False
+    c.append_kv(1, 0, np.zeros((2, 8), np.float32), np.zeros((2, 8), np.float32))
+    if c.block_table[1, 0] != 5:
+        return False
+    c2 = ora.RefPagedKVCache(1, 1, 1, 4, 1, 8, "f16")
+    c2.allocate_sequence()
+    for _ in range(16):
+        c2.append_kv(0, 0, np.zeros((1, 8), np.float32), np.zeros((1, 8), np.float32))
+    try:
+        c2.append_kv(0, 0, np.zeros((1, 8), np.float32), np.zeros((1, 8), np.float32))
+        return False
+    except RuntimeError as e:
+        return "Out of KV pages" in str(e)
+
+
 PINS = [pin_sdpa, pin_exp_sink, pin_linear_sink, pin_golden_varlen, pin_golden_paged,
-        pin_split_merge, pin_closed_forms, pin_layouts, pin_gather]
+        pin_split_merge, pin_closed_forms, pin_layouts, pin_gather, pin_kv_encode, pin_paged_write,
+        pin_ref_cache]
 
 
 @pytest.mark.parametrize("pin", PINS, ids=lambda f: f.__name__)
@@ -303,6 +398,42 @@ def _merge_no_weight(acc, m, l, sink=None, sink_mode="exp"):
     return num / den[:, None]
 
 
+def _store_rows_transposed(pool, slots, rows):
+    P, Hkv, ps, D = pool.shape
+    rows = np.asarray(rows).reshape(-1, Hkv, D)
+    for i, s in enumerate(np.asarray(slots, dtype=np.int64).reshape(-1)):
+        if 0 <= s < P * ps:
+            pool[s % P, :, s // P % ps, :] = rows[i]
+    return pool
+
+
+def _bf16_truncate(x):
+    return (np.asarray(x, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+_e4m3_encode_orig = O.e4m3_encode
+_encode_kv_orig = O.encode_kv
+
+
+def _e4m3_encode_tie_to_nan(x):
+    x = np.asarray(x, dtype=np.float64)
+    codes = _e4m3_encode_orig(x)
+    return np.where(np.abs(x) == 464.0, codes | 0x7F, codes).astype(np.uint8)
+
+
+def _encode_kv_no_clamp(x, pool_dtype, scale=None):
+    if pool_dtype == "e4m3" and scale is not None:
+        return _e4m3_encode_orig(np.asarray(x, dtype=np.float32) / np.float32(scale))
+    return _encode_kv_orig(x, pool_dtype, scale)
+
+
+class _FifoCache(O.RefPagedKVCache):
+    def append_kv(self, sid, layer, k, v):
+        if self.seq_lens[sid] % self.page_size == 0 and self.free_pages:
+            self.free_pages.insert(len(self.free_pages), self.free_pages.pop(0))
+        super().append_kv(sid, layer, k, v)
+
+
 MUTANTS = {
     "head mapping h % Hkv": Mutant(attend=_attend_variant("headmap")),
     "sm_scale dropped": Mutant(attend=_attend_variant("noscale")),
@@ -311,6 +442,11 @@ MUTANTS = {
     "page index transposed": Mutant(paged_rows=_paged_rows_transposed),
     "varlen off by one": Mutant(decode_varlen=_varlen_off_by_one),
     "LSE weight dropped": Mutant(merge_partials=_merge_no_weight),
+    "write slot transposed": Mutant(paged_store_rows=_store_rows_transposed),
+    "bf16 truncated": Mutant(bf16_bits=_bf16_truncate),
+    "e4m3 tie at 464 encodes NaN": Mutant(e4m3_encode=_e4m3_encode_tie_to_nan),
+    "quantiser without clamp": Mutant(encode_kv=_encode_kv_no_clamp),
+    "free list FIFO": Mutant(RefPagedKVCache=_FifoCache),
 }
 
 

@@ -1,5 +1,8 @@
-"""PagedKVCache host logic on CPU tensors (same API and state transitions as
-fskernels/paged_attn/paged_kv_cache.py:6-154)."""
+"""PagedKVCache host logic on the CPU: page bookkeeping, block-table stores and
+slots, against the oracle's restatement of fskernels/paged_attn/paged_kv_cache.py
+(RefPagedKVCache).  Row stores need the HIP write kernel and are covered by the
+GPU tests; here they must refuse to run."""
+import random
 import types
 
 import numpy as np
@@ -10,12 +13,17 @@ from fasterkernels_amd.paged_attn import PAGE_SIZE, PagedKVCache
 from oracle import decode_oracle as O
 
 
-def make(num_pages=8, max_seqs=3, max_blocks=4, layers=2, hkv=2, d=8):
-    return PagedKVCache(layers, num_pages, max_seqs, max_blocks, hkv, d, torch.float32, "cpu")
+def make(num_pages=8, max_seqs=3, max_blocks=4, layers=2, hkv=2, d=8, dtype=torch.float16):
+    return PagedKVCache(layers, num_pages, max_seqs, max_blocks, hkv, d, dtype, "cpu")
 
 
-def kv(hkv=2, d=8, val=0.0):
-    return torch.full((1, hkv, 1, d), val), torch.full((1, hkv, 1, d), -val)
+def bt_after(cache, updates):
+    """The block table the device would hold after the planned stores."""
+    bt = cache.block_table.clone().view(-1)
+    for flat, page in updates:
+        bt[flat] = page
+    cache.block_table.copy_(bt.view_as(cache.block_table))
+    return cache.block_table
 
 
 def test_layout_and_init():
@@ -36,81 +44,147 @@ def test_slots_lowest_first_and_exhaustion():
     assert c.allocate_sequence() == 1
 
 
-def test_append_allocates_pages_lifo_at_boundaries():
+def test_plan_matches_reference_bookkeeping():
+    """One token at a time: the same pages, block table and lengths as the
+    reference's append_kv, and slots that address the reference's rows."""
     c = make()
+    ref = O.RefPagedKVCache(1, 8, 3, 4, 2, 8, "f16")
     s = c.allocate_sequence()
+    assert ref.allocate_sequence() == s
     for pos in range(33):
-        k, v = kv(val=float(pos + 1))
-        c.append_kv(s, 0, k, v)
-    # pages come off the end of the free list: 7, 6, 5
-    assert c.block_table[s, :4].tolist() == [7, 6, 5, -1]
-    assert c.pages_used == 3
+        slots, upd = c._plan([s])
+        ref.append_kv(s, 0, np.zeros((2, 8), np.float32), np.zeros((2, 8), np.float32))
+        bt_after(c, upd)
+        page = ref.block_table[s, pos // 16]
+        assert slots == [page * 16 + pos % 16]
+    assert c.block_table[s].tolist() == ref.block_table[s].tolist() == [7, 6, 5, -1]
     assert c.get_seq_lens_tensor([s]).tolist() == [33]
-    # token 17 lives in page block_table[s, 1] at row 1
-    assert torch.equal(c.k_pool[0, 6, :, 1, :], torch.full((2, 8), 18.0))
-    assert torch.equal(c.v_pool[0, 5, :, 0, :], torch.full((2, 8), -33.0))
+    assert c.pages_used == 3
 
 
 def test_free_returns_pages_in_logical_order():
     c = make()
     s = c.allocate_sequence()
-    for pos in range(20):
-        c.append_kv(s, 0, *kv())
+    bt_after(c, c._plan([s], 20)[1])
     c.free_sequence(s)
     assert (c.block_table[s] == -1).all()
     assert c.pages_free == 8
-    # freed pages 7, 6 appended in logical order -> next allocation pops 6
     s2 = c.allocate_sequence()
-    c.append_kv(s2, 0, *kv())
-    assert c.block_table[s2, 0].item() == 6
+    slots, upd = c._plan([s2])
+    assert upd == [(s2 * 4 + 0, 6)] and slots == [6 * 16]   # freed 7, 6 in logical order -> pops 6
 
 
-def test_out_of_pages():
+def test_out_of_pages_is_all_or_nothing():
     c = make(num_pages=2)
     s = c.allocate_sequence()
-    for pos in range(32):
-        c.append_kv(s, 0, *kv())
+    c._plan([s], 32)
     with pytest.raises(RuntimeError, match="Out of KV pages"):
-        c.append_kv(s, 0, *kv())
+        c._plan([s])
+    assert c._seq_lens[s] == 32 and c.pages_free == 0
+    # a batch that needs more pages than are free changes nothing
+    c2 = make(num_pages=3)
+    a, b = c2.allocate_sequence(), c2.allocate_sequence()
+    with pytest.raises(RuntimeError, match="Out of KV pages"):
+        c2._plan([a, b], 17)          # 2 + 2 pages
+    assert c2.pages_free == 3 and c2._seq_lens[a] == c2._seq_lens[b] == 0
 
 
-def test_block_table_rows_and_lengths():
+def test_block_table_width_is_checked_before_any_change():
+    c = make(num_pages=16, max_blocks=2)
+    s = c.allocate_sequence()
+    with pytest.raises(IndexError):
+        c._plan([s], 33)
+    assert c.pages_free == 16 and c._seq_lens[s] == 0
+
+
+def test_random_batches_match_per_token_reference():
+    """Batched plans (repeated ids, multi-token reservations, frees) give the
+    state a sequence of reference append_kv calls gives."""
+    rnd = random.Random(7)
+    for trial in range(20):
+        P, S, MB = 40, 5, 6
+        c = make(num_pages=P, max_seqs=S, max_blocks=MB, layers=1)
+        ref = O.RefPagedKVCache(1, P, S, MB, 2, 8, "f16")
+        live = []
+        for step in range(30):
+            op = rnd.random()
+            if op < 0.15 and len(live) < S:
+                sid = c.allocate_sequence()
+                assert ref.allocate_sequence() == sid
+                live.append(sid)
+            elif op < 0.25 and live:
+                sid = live.pop(rnd.randrange(len(live)))
+                c.free_sequence(sid)
+                ref.free_sequence(sid)
+            elif live:
+                ids = [rnd.choice(live) for _ in range(rnd.randint(1, 4))]
+                n_tok = rnd.choice([1, 1, 3, 17])
+                total_after = {i: ref.seq_lens[i] + n_tok * ids.count(i) for i in set(ids)}
+                need = sum(-(-total_after[i] // 16) - -(-ref.seq_lens[i] // 16) for i in set(ids))
+                if need > len(ref.free_pages) or max(-(-v // 16) for v in total_after.values()) > MB:
+                    with pytest.raises((RuntimeError, IndexError)):
+                        c._plan(ids, n_tok)
+                    continue
+                slots, upd = c._plan(ids, n_tok)
+                bt_after(c, upd)
+                want = []
+                for i in ids:
+                    for _ in range(n_tok):
+                        pos = ref.seq_lens[i]
+                        ref.append_kv(i, 0, np.zeros((2, 8), np.float32), np.zeros((2, 8), np.float32))
+                        want.append(int(ref.block_table[i, pos // 16]) * 16 + pos % 16)
+                assert slots == want
+            assert c.block_table.numpy().tolist() == ref.block_table.tolist()
+            assert c._seq_lens == ref.seq_lens and c._free_pages == ref.free_pages
+
+
+def test_planned_slots_decode_like_dense_attention():
+    """Rows stored at the planned slots (oracle store) and read back with the
+    oracle's paged addressing give the dense sequences' attention."""
+    g = np.random.default_rng(0)
+    hkv, d, hq = 2, 16, 8
+    c = make(num_pages=12, max_seqs=3, max_blocks=4, layers=1, hkv=hkv, d=d)
+    lens = [5, 40, 17]
+    sids = [c.allocate_sequence() for _ in lens]
+    pool_k = np.zeros((12, hkv, 16, d), np.float16)
+    pool_v = np.zeros_like(pool_k)
+    dense = []
+    for s, L in zip(sids, lens):
+        ks = g.standard_normal((L, hkv, d)).astype(np.float16).astype(np.float32)
+        vs = g.standard_normal((L, hkv, d)).astype(np.float16).astype(np.float32)
+        slots, upd = c._plan([s], L)
+        bt_after(c, upd)
+        O.paged_write(pool_k, slots, ks, "f16")
+        O.paged_write(pool_v, slots, vs, "f16")
+        dense.append((ks, vs))
+    q = g.standard_normal((3, hq, d))
+    bt = c.get_block_table_tensor(sids).numpy()
+    got = O.decode_paged(q, pool_k.astype(np.float32), pool_v.astype(np.float32), bt, lens)
+    want = np.stack([O.attend(q[i], *dense[i]) for i in range(3)])
+    assert np.allclose(got, want, atol=1e-12)
+
+
+def test_row_stores_refuse_host_pools():
     c = make()
-    a, b = c.allocate_sequence(), c.allocate_sequence()
-    for _ in range(3):
-        c.append_kv(a, 0, *kv())
-    for _ in range(17):
-        c.append_kv(b, 0, *kv())
-    bt = c.get_block_table_tensor([b, a])
-    assert bt.shape == (2, 4) and bt.dtype == torch.int32
-    assert bt[0, :2].tolist() == c.block_table[b, :2].tolist()
-    assert c.get_seq_lens_tensor([b, a]).tolist() == [17, 3]
+    s = c.allocate_sequence()
+    k = torch.zeros(1, 2, 1, 8, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="not a GPU"):
+        c.append_kv(s, 0, k, k)
+    with pytest.raises(RuntimeError, match="not a GPU"):
+        c.reserve_slots([s])
+    assert c._seq_lens[s] == 0 and c.pages_free == 8   # nothing was planned
+
+
+def test_scales_only_for_e4m3_pools():
+    with pytest.raises(ValueError):
+        PagedKVCache(1, 2, 1, 1, 1, 8, torch.float16, "cpu", k_scale=0.5, v_scale=0.5)
+    with pytest.raises(ValueError):
+        PagedKVCache(1, 2, 1, 1, 1, 8, torch.float8_e4m3fn, "cpu", k_scale=0.5)
+    c = PagedKVCache(1, 2, 1, 1, 1, 8, torch.float8_e4m3fn, "cpu", k_scale=0.5, v_scale=0.25)
+    assert c.k_scale.dtype == torch.float32 and c.k_scale.item() == 0.5 and c.v_scale.item() == 0.25
 
 
 def test_from_config_uses_bf16():
     cfg = types.SimpleNamespace(num_hidden_layers=3, num_key_value_heads=4, head_dim=64)
     c = PagedKVCache.from_config(cfg, num_pages=5, max_seqs=2, max_blocks_per_seq=3, device="cpu")
     assert c.k_pool.dtype == torch.bfloat16 and c.k_pool.shape == (3, 5, 4, 16, 64)
-
-
-def test_cache_layout_decodes_like_dense_attention():
-    """Tokens appended through the cache, read back with the oracle's paged
-    addressing, give the same attention as the dense sequences."""
-    g = torch.Generator().manual_seed(0)
-    hkv, d, hq = 2, 16, 8
-    c = make(num_pages=12, max_seqs=3, max_blocks=4, layers=1, hkv=hkv, d=d)
-    lens = [5, 40, 17]
-    dense_k, dense_v = [], []
-    sids = [c.allocate_sequence() for _ in lens]
-    for s, L in zip(sids, lens):
-        ks = torch.randn(L, hkv, d, generator=g)
-        vs = torch.randn(L, hkv, d, generator=g)
-        for t in range(L):
-            c.append_kv(s, 0, ks[t][None, :, None, :], vs[t][None, :, None, :])
-        dense_k.append(ks.numpy())
-        dense_v.append(vs.numpy())
-    q = torch.randn(3, hq, d, generator=g).numpy()
-    bt = c.get_block_table_tensor(sids).numpy()
-    got = O.decode_paged(q, c.k_pool[0].numpy(), c.v_pool[0].numpy(), bt, lens)
-    want = np.stack([O.attend(q[i], dense_k[i], dense_v[i]) for i in range(3)])
-    assert np.allclose(got, want, atol=1e-12)
