@@ -32,7 +32,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="M0", help="workload name (M0, C1..C5)")
+    ap.add_argument("--config", default="M0", help="workload name (decode: M0, C1..C5; KV write: W0..W2)")
     ap.add_argument("--sets", type=int, default=0, help="input sets to rotate (0: enough for >1 GB)")
     ap.add_argument("--chunk", type=int, default=0, help="split size in tokens (0: library default)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
@@ -127,6 +127,117 @@ def cpu_baseline(wl, budget_s: float):
     }
 
 
+def cpu_baseline_write(wl, budget_s: float):
+    """Times the numpy oracle's row store on a bounded sample of ``wl``'s tokens."""
+    import numpy as np
+    import torch
+
+    from oracle import decode_oracle as O
+
+    n = min(wl.tokens, 2048)
+    x_k = wl.k[:n].float().cpu().numpy()
+    x_v = wl.v[:n].float().cpu().numpy()
+    slots = wl.slots[:n].cpu().numpy()
+    pool_dt = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float8_e4m3fn: "e4m3"}[wl.k_pool.dtype]
+    shape = tuple(wl.k_pool.shape)
+    kp = np.zeros(shape, dtype=O._POOL_NP[pool_dt])
+    vp = np.zeros_like(kp)
+    ks = None if wl.k_scale is None else np.float32(wl.k_scale.item())
+    vs = None if wl.v_scale is None else np.float32(wl.v_scale.item())
+
+    def step():
+        O.paged_write(kp, slots, x_k, pool_dt, ks)
+        O.paged_write(vp, slots, x_v, pool_dt, vs)
+    step()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    per_tok = wl.k.shape[1] * wl.k.shape[2] * 2 * (wl.k.element_size() + wl.k_pool.element_size()) + 8
+    return {
+        "value": round(n * per_tok / med / 1e9, 4),
+        "unit": "GB/s",
+        "us_per_step_extrapolated": round(med * 1e6 * wl.tokens / n, 1),
+        "cores": 1,
+        "kind": "port",
+        "sample": f"numpy oracle row store, first {n} of {wl.tokens} tokens of {wl.name}, "
+                  f"median of {len(times)} runs",
+    }
+
+
+def bench_write(args):
+    """The KV write path: one store of a batch of rows into scattered pages."""
+    import torch
+
+    from fasterkernels_amd import workloads as W
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    base = W.make_write(args.config, device=dev)
+    alg_bytes = base.algorithmic_bytes()
+    n_sets = args.sets or max(1, min(8, -(-1_100_000_000 // alg_bytes)))
+    sets = [base] + [W.make_write(args.config, device=dev, data_seed=base.meta["seed"] + 1000 * i)
+                     for i in range(1, n_sets)]
+    for i in range(args.warmup):
+        W.run_write(sets[i % n_sets])
+    torch.cuda.synchronize()
+    evs = []
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        rec = i % 8 == 0
+        if rec:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+        W.run_write(sets[i % n_sets])
+        if rec:
+            b.record()
+            evs.append((a, b))
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kern_ms = statistics.mean(a.elapsed_time(b) for a, b in evs)
+    ms_step = elapsed * 1e3 / args.steps
+    gbs = alg_bytes / (ms_step / 1e3) / 1e9
+    kern_gbs = alg_bytes / (kern_ms / 1e3) / 1e9
+    cfg = base.meta
+    out = {
+        "metric": f"KV write achieved HBM GB/s (rows read + written), {args.config}",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "us_per_step": round(ms_step * 1e3, 2),
+        "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": f"{cfg['src']}->{cfg['pool']}",
+        "data": f"synthetic N(0,1), generated on device, {n_sets} rotating input sets",
+        "config": {
+            "workload": f"{args.config}: paged KV write of {base.tokens} tokens x Hkv={base.k.shape[1]} "
+                        f"x D={base.k.shape[2]}, {cfg['src']} rows -> {cfg['pool']} pools"
+                        + (" (fixed-scale quantisation)" if cfg["scaled"] else ""),
+            "tokens": base.tokens, "algorithmic_bytes": alg_bytes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(kern_gbs, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(kern_gbs / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "kernel": "kv_write_kernel",
+            "kernel_avg_us": round(kern_ms * 1e3, 3),
+        },
+        "cpu_baseline": None if args.no_cpu else cpu_baseline_write(base, args.cpu_seconds),
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -144,6 +255,9 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no HIP GPU visible"}))
         sys.exit(2)
+    if args.config in W.WRITE_CONFIGS:
+        bench_write(args)
+        return
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     base = W.make(args.config, gen_device=dev, device=dev)

@@ -868,17 +868,39 @@ struct WriteParams {
 };
 
 constexpr int kWriteThreads = 256;
-constexpr int kWriteUnroll = 4;
+#ifndef FSK_WRITE_UNROLL
+#define FSK_WRITE_UNROLL 4
+#endif
+#ifndef FSK_WRITE_BLOCKS_PER_CU
+#define FSK_WRITE_BLOCKS_PER_CU 16
+#endif
+// Cache policy of the write kernel's row loads and stores: 0 default, 1
+// non-temporal (each row is read once and written once).
+#ifndef FSK_WRITE_NT
+#define FSK_WRITE_NT 0
+#endif
+constexpr int kWriteUnroll = FSK_WRITE_UNROLL;
+
+template <typename T>
+__device__ __forceinline__ T row_load(const T* p) {
+  if constexpr (FSK_WRITE_NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <typename T>
+__device__ __forceinline__ void row_store(T* p, T x) {
+  if constexpr (FSK_WRITE_NT) __builtin_nontemporal_store(x, p);
+  else *p = x;
+}
 
 template <int kSrc>
 __device__ __forceinline__ void load8(const uint8_t* p, float (&x)[8], u32x4& raw) {
   if constexpr (kSrc == kF32) {
-    const f32x4 a = *(const f32x4*)p;
-    const f32x4 b = *(const f32x4*)(p + 16);
+    const f32x4 a = row_load((const f32x4*)p);
+    const f32x4 b = row_load((const f32x4*)(p + 16));
     x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
     x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
   } else {
-    raw = *(const u32x4*)p;
+    raw = row_load((const u32x4*)p);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       // The element goes through a scalar: this compiler lowers
@@ -897,19 +919,33 @@ __device__ __forceinline__ void load8(const uint8_t* p, float (&x)[8], u32x4& ra
   }
 }
 
+// x / s rounded to fp32, for fp32 x and a scale s (finite, nonzero), from
+// rs = RN64(1 / s) as RN32(RN64(x * rs)).  This equals the correctly rounded
+// fp32 quotient: with x = X 2^a and s = S 2^b (X, S odd, < 2^24) the exact
+// quotient is never an fp32 rounding midpoint (a midpoint has 25 significant
+// bits, so m s = x would need an odd factor >= 2^24 + 1 in X) and lies at a
+// relative distance >= 1 / (2 S 2^24) >= 2^-49 from every midpoint, while the
+// two binary64 roundings perturb it by at most 2^-52 (1 + 2^-53) relative.
+// Quotients in the fp32 subnormal range may differ, but they all quantise to
+// a signed zero below.  Costs a convert, a multiply and a convert instead of
+// the ten-instruction fp32 division sequence.
+__device__ __forceinline__ float div_by_scale(float x, double rs) {
+  return (float)((double)x * rs);
+}
+
 // Four fp32 values -> four e4m3fn codes (round to nearest even, as torch's
-// float8_e4m3fn cast).  With a scale the values are first divided by it and
-// clamped to +-448 (the quantiser of
-// fskernels/triton/triton_gqa_decode_hf_fp8.py:13-16); without one they are
-// cast as they are, so magnitudes above 464 encode NaN as the cast does.  NaN
-// inputs give 0x7F with the input's sign bit, as the cast does.
+// float8_e4m3fn cast).  With a scale the values are first divided by it
+// (rs = 1 / scale in binary64, see div_by_scale) and clamped to +-448 (the
+// quantiser of fskernels/triton/triton_gqa_decode_hf_fp8.py:13-16); without one
+// they are cast as they are, so magnitudes above 464 encode NaN as the cast
+// does.  NaN inputs give 0x7F with the input's sign bit, as the cast does.
 template <bool kScaled>
-__device__ __forceinline__ uint32_t encode_e4m3x4(const float* x, float s) {
+__device__ __forceinline__ uint32_t encode_e4m3x4(const float* x, double rs) {
   float y[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     y[j] = x[j];
-    if constexpr (kScaled) y[j] = fminf(fmaxf(x[j] / s, -E4M3_MAX_F), E4M3_MAX_F);
+    if constexpr (kScaled) y[j] = fminf(fmaxf(div_by_scale(x[j], rs), -E4M3_MAX_F), E4M3_MAX_F);
   }
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w, true);
@@ -953,8 +989,8 @@ __global__ __launch_bounds__(kWriteThreads) void kv_write_kernel(WriteParams p) 
   uint8_t* pool = p.pool[kv] + g * kDstBytes;
   const int64_t s_st = p.s_st[kv], s_sh = p.s_sh[kv];
   const int64_t p_sp = p.p_sp[kv], p_sh = p.p_sh[kv], p_st = p.p_st[kv];
-  float scale = 1.f;
-  if constexpr (kScaled) scale = *p.scale[kv];
+  double rscale = 1.0;
+  if constexpr (kScaled) rscale = 1.0 / (double)*p.scale[kv];
   const uint32_t step = gridDim.x * rows_per_block;
   for (uint32_t r0 = blockIdx.x * rows_per_block + lrow; r0 < p.rows; r0 += step * kWriteUnroll) {
     float x[kWriteUnroll][8];
@@ -979,12 +1015,12 @@ __global__ __launch_bounds__(kWriteThreads) void kv_write_kernel(WriteParams p) 
       if (doff[u] < 0) continue;
       uint8_t* dst = pool + doff[u];
       if constexpr (kPool == kE4M3) {
-        *(u32x2*)dst = u32x2{encode_e4m3x4<kScaled>(x[u], scale), encode_e4m3x4<kScaled>(x[u] + 4, scale)};
+        row_store((u32x2*)dst, u32x2{encode_e4m3x4<kScaled>(x[u], rscale), encode_e4m3x4<kScaled>(x[u] + 4, rscale)});
       } else if constexpr (kPool == kSrc) {
-        *(u32x4*)dst = raw[u];  // same type: a bit-exact copy
+        row_store((u32x4*)dst, raw[u]);  // same type: a bit-exact copy
       } else {
-        *(u32x4*)dst = u32x4{pack2<kPool>(x[u][0], x[u][1]), pack2<kPool>(x[u][2], x[u][3]),
-                             pack2<kPool>(x[u][4], x[u][5]), pack2<kPool>(x[u][6], x[u][7])};
+        row_store((u32x4*)dst, u32x4{pack2<kPool>(x[u][0], x[u][1]), pack2<kPool>(x[u][2], x[u][3]),
+                                     pack2<kPool>(x[u][4], x[u][5]), pack2<kPool>(x[u][6], x[u][7])});
       }
     }
   }
@@ -1365,7 +1401,7 @@ int run_write(const WriteArgs& a) {
   p.bt = a.bt; p.bt_numel = a.bt_numel; p.upd = a.upd; p.n_upd = (int)a.n_upd;
   const int64_t rows_per_block = kWriteThreads / p.groups;
   const int64_t blocks = std::min<int64_t>(std::max<int64_t>(cdiv(p.rows, rows_per_block * kWriteUnroll), 1),
-                                           (int64_t)device_cus() * 8);
+                                           (int64_t)device_cus() * FSK_WRITE_BLOCKS_PER_CU);
   const dim3 grid((unsigned)blocks, 2);
   (void)hipGetLastError();
   if (a.src_dt == FSK_F16) dispatch_write<kF16>(p, a.pool_dt, scaled, grid, a.stream);

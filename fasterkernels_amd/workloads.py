@@ -197,3 +197,72 @@ def run(wl: Workload, *, sink_mode: str = "exp", chunk_tokens: int = 0):
     return dec.flash_decode_gqa_varlen(wl.q, wl.k, wl.v, wl.cu_seqlens, wl.s_aux,
                                        sink_mode=sink_mode, k_scale=wl.k_scale, v_scale=wl.v_scale,
                                        out_dtype=wl.out_dtype, chunk_tokens=chunk_tokens)
+
+
+# ---------------------------------------------------------------------------
+# KV write workloads: new rows stored into paged pools at scattered slots
+# ---------------------------------------------------------------------------
+WRITE_CONFIGS = {
+    # the whole M0 cache (4 x 32768 tokens) stored in one launch, f16 -> f16 pools
+    "W0": dict(src="f16", pool="f16", B=4, L=32768, Hkv=8, D=128, scaled=False, seed=110),
+    # the same rows from bf16 projections quantised into e4m3 pools (C4/C5 pools)
+    "W1": dict(src="bf16", pool="e4m3", B=4, L=32768, Hkv=8, D=128, scaled=True, seed=111),
+    # one decode step's append: one token for each of C5's 64 sequences
+    "W2": dict(src="bf16", pool="e4m3", B=64, L=1, Hkv=8, D=128, scaled=True, seed=112),
+}
+
+
+@dataclass
+class WriteWorkload:
+    name: str
+    k: torch.Tensor              # [n, Hkv, D] new rows
+    v: torch.Tensor
+    slots: torch.Tensor          # int64 [n]
+    k_pool: torch.Tensor         # [P, Hkv, 16, D]
+    v_pool: torch.Tensor
+    k_scale: torch.Tensor | None
+    v_scale: torch.Tensor | None
+    meta: dict = field(default_factory=dict)
+
+    @property
+    def tokens(self) -> int:
+        return self.k.shape[0]
+
+    def algorithmic_bytes(self) -> int:
+        """Rows read + rows written + slots (+ scales)."""
+        n, hkv, d = self.k.shape
+        b = n * hkv * d * 2 * (self.k.element_size() + self.k_pool.element_size()) + 8 * n
+        return b + (8 if self.k_scale is not None else 0)
+
+
+def make_write(name: str, *, device, data_seed: int | None = None) -> WriteWorkload:
+    """Rows for sequences of L tokens laid out on a shuffled pool with 10 %
+    spare pages; token t of sequence b goes to its page t // 16, row t % 16."""
+    cfg = WRITE_CONFIGS[name]
+    B, L, hkv, d = cfg["B"], cfg["L"], cfg["Hkv"], cfg["D"]
+    dev = torch.device(device)
+    g = torch.Generator(device=dev).manual_seed(cfg["seed"] if data_seed is None else data_seed)
+    pages_per_seq = (L + PAGE - 1) // PAGE
+    P = B * pages_per_seq + max(1, B * pages_per_seq // 10)
+    gp = torch.Generator(device=dev).manual_seed(cfg["seed"])
+    perm = torch.randperm(P, device=dev, generator=gp)[:B * pages_per_seq].view(B, pages_per_seq)
+    # a decode-step append writes the next row of partly filled pages
+    t = torch.arange(L, device=dev) + (7 if L == 1 else 0)
+    slots = (perm[:, t // PAGE] * PAGE + t % PAGE).reshape(-1).to(torch.int64)
+    src = DTYPES[cfg["src"]]
+    k = torch.randn(B * L, hkv, d, device=dev, generator=g).to(src)
+    v = torch.randn(B * L, hkv, d, device=dev, generator=g).to(src)
+    pool = DTYPES[cfg["pool"]]
+    kp = torch.zeros(P, hkv, PAGE, d, dtype=pool, device=dev)
+    vp = torch.zeros_like(kp)
+    ks = vs = None
+    if cfg["scaled"]:
+        ks = torch.tensor(4.0 / 448.0, dtype=torch.float32, device=dev)
+        vs = torch.tensor(4.0 / 448.0, dtype=torch.float32, device=dev)
+    return WriteWorkload(name, k, v, slots, kp, vp, ks, vs, dict(cfg, num_pages=P))
+
+
+def run_write(wl: WriteWorkload) -> None:
+    """One store of ``wl``'s rows through the HIP write entry point."""
+    from .hip.kv_write import paged_kv_write
+    paged_kv_write(wl.k, wl.v, wl.k_pool, wl.v_pool, wl.slots, k_scale=wl.k_scale, v_scale=wl.v_scale)

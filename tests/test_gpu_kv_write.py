@@ -110,6 +110,40 @@ def test_write_matches_oracle(src, pool, scaled):
     compare(vg, vo, pool, src, f"V {src}->{pool} scaled={scaled}")
 
 
+def _scales():
+    fixed = [1.0, 0.5, 3.0, 1 / 3, 0.1, 0.0123, 4 / 448, 448 / 65504, 1e-3, 7.77e-5, 1e-8, 1e-30, 2.5e30,
+             1.0000001, 0.99999994, 1e-40, 2.0 ** -126, 3.4e38]
+    g = torch.Generator().manual_seed(77)
+    rand = torch.exp(torch.empty(18).uniform_(-14.0, 9.0, generator=g)).tolist()
+    return [float(torch.tensor(v, dtype=torch.float32)) for v in fixed + rand]
+
+
+@pytest.mark.parametrize("src", ["f16", "bf16", "f32"])
+def test_quantiser_is_exact_for_every_source_value(src):
+    """e4m3 codes of every f16 / bf16 bit pattern (and 2^20 random f32
+    patterns) under 36 scales equal torch's evaluation of the reference
+    quantiser, (x.float() / scale).clamp(-448, 448).to(float8_e4m3fn)."""
+    if src == "f32":
+        bits32 = torch.randint(-(1 << 31), 1 << 31, (1 << 20,), generator=torch.Generator().manual_seed(5),
+                               dtype=torch.int64).to(torch.int32)
+        x = bits32.view(torch.float32)
+    else:
+        x = torch.arange(-(1 << 15), 1 << 15, dtype=torch.int32).to(torch.int16).view(SRC[src])
+    d = 128
+    rows = x.reshape(-1, 1, d)
+    n = rows.shape[0]
+    pool = torch.empty(n, 1, 16, d, dtype=torch.float8_e4m3fn, device=DEV)
+    slots = (torch.arange(n) * 16).to(DEV)
+    rows_g = rows.to(DEV)
+    for scale in _scales():
+        st = torch.tensor(scale, dtype=torch.float32)
+        paged_kv_write(rows_g, rows_g, pool, pool, slots, k_scale=st.to(DEV), v_scale=st.to(DEV))
+        got = pool[:, 0, 0, :].reshape(-1).view(torch.uint8).cpu()
+        want = (x.float() / st).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8)
+        bad = got != want
+        assert not bad.any(), (scale, x[bad][:4].tolist(), got[bad][:4].tolist(), want[bad][:4].tolist())
+
+
 @pytest.mark.parametrize("d", [64, 128, 256, 136])
 def test_head_dims_and_strided_sources(d):
     """HF projections arrive as [1, Hkv, L, D]; the [L, Hkv, D] view of one is
