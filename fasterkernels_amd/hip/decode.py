@@ -251,7 +251,7 @@ def flash_decode_gqa_hf_dense_optimized(q, k_cache, v_cache, cache_lens, start_k
 
 
 def flash_decode_gqa_hf_fp8(q_fp8, k_cache_fp8, v_cache_fp8, cache_lens, scale_q, scale_k,
-                            scale_v, out_dtype):
+                            scale_v, out_dtype, *, start_k_offsets=None, sm_scale: float | None = None):
     """FP8 e4m3 dense decode with per-tensor scales.
 
     Reference: fskernels/triton/triton_gqa_decode_hf_fp8.py:164-227.  q_fp8
@@ -259,10 +259,13 @@ def flash_decode_gqa_hf_fp8(q_fp8, k_cache_fp8, v_cache_fp8, cache_lens, scale_q
     0-dim fp32 device tensors (dequantised value = code * scale).  Q is
     dequantised to fp16 as the reference does (:47-50); K/V are dequantised
     exactly in registers and their scales applied in fp32.  Returns
-    [B, Hq, D] in ``out_dtype``.
+    [B, Hq, D] in ``out_dtype``.  Keyword-only additions: ``start_k_offsets``
+    (attend [start, cache_len) as the fp16/bf16 dense entry does) and
+    ``sm_scale`` (default 1/sqrt(D)).
     """
-    return _dense(q_fp8, k_cache_fp8, v_cache_fp8, cache_lens, None, _DECODE_NUM_SPLITS_FP8,
-                  q_scale=scale_q, k_scale=scale_k, v_scale=scale_v, out_dtype=out_dtype)
+    return _dense(q_fp8, k_cache_fp8, v_cache_fp8, cache_lens, start_k_offsets, _DECODE_NUM_SPLITS_FP8,
+                  q_scale=scale_q, k_scale=scale_k, v_scale=scale_v, out_dtype=out_dtype,
+                  sm_scale=sm_scale)
 
 
 # ---------------------------------------------------------------------------
