@@ -35,6 +35,8 @@ def parse():
     ap.add_argument("--config", default="M0", help="workload name (decode: M0, C1..C5; KV write: W0..W2)")
     ap.add_argument("--sets", type=int, default=0, help="input sets to rotate (0: enough for >1 GB)")
     ap.add_argument("--chunk", type=int, default=0, help="split size in tokens (0: library default)")
+    ap.add_argument("--graph", action="store_true",
+                    help="replay each decode step from a captured HIP graph (no per-step host work)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
@@ -269,28 +271,55 @@ def main():
     assert all(s.lens == base.lens for s in sets)
     alg_bytes = base.algorithmic_bytes()
 
-    def step(i):
-        return W.run(sets[i % n_sets], chunk_tokens=args.chunk)
+    if args.graph:
+        from fasterkernels_amd.graph import DecodeGraph
+        graphs = [DecodeGraph(W.run, s, chunk_tokens=args.chunk) for s in sets]
+
+        def step(i):
+            return graphs[i % n_sets].replay()
+    else:
+        def step(i):
+            return W.run(sets[i % n_sets], chunk_tokens=args.chunk)
 
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    # kernel durations: HIP events on one call in 8 of the timed region
-    nat.enable_kernel_timing(8)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    part_ms, tot_ms, calls = nat.kernel_timing()
-    nat.enable_kernel_timing(0)
+    if args.graph:
+        # the library's event hook does not run inside a replay: time 1 replay in 8 with events
+        evs = []
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            if i % 8 == 0:
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                step(i)
+                b.record()
+                evs.append((a, b))
+            else:
+                step(i)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        tot_ms = sum(a.elapsed_time(b) for a, b in evs)
+        part_ms, calls = 0.0, len(evs)
+    else:
+        # kernel durations: HIP events on one call in 8 of the timed region
+        nat.enable_kernel_timing(8)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step(i)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        part_ms, tot_ms, calls = nat.kernel_timing()
+        nat.enable_kernel_timing(0)
 
     ms_step = elapsed * 1e3 / args.steps
     gbs = alg_bytes / (ms_step / 1e3) / 1e9
     part_avg_ms = part_ms / max(calls, 1)
+    if args.graph:   # the replay (partial + reduce) is the timed unit
+        part_avg_ms = tot_ms / max(calls, 1)
     kern_gbs = alg_bytes / (part_avg_ms / 1e3) / 1e9 if part_avg_ms > 0 else None
-    traffic = read_traffic(args.traffic) if args.config == "M0" and not args.chunk else None
+    traffic = read_traffic(args.traffic) if args.config == "M0" and not args.chunk and not args.graph else None
 
     out = {
         "metric": METRIC,
@@ -312,6 +341,7 @@ def main():
                         f"D={base.D} tokens={base.total_tokens} kv={str(base.k.dtype).replace('torch.', '')}",
             "batch": base.B, "total_tokens": base.total_tokens, "algorithmic_bytes": alg_bytes,
             "chunk_tokens": args.chunk or "auto",
+            "launch": "hip graph replay" if args.graph else "eager",
         },
         "roofline": {
             "bound": "hbm",
@@ -320,7 +350,8 @@ def main():
             "unit": "GB/s",
             "frac": None if kern_gbs is None else round(kern_gbs / PEAK_HBM_GBS, 4),
             "traffic": traffic,
-            "kernel": "partial_kernel (split-KV partials)",
+            "kernel": ("partial_kernel + reduce_kernel (one graph replay)" if args.graph
+                       else "partial_kernel (split-KV partials)"),
             "kernel_avg_us": round(part_avg_ms * 1e3, 3),
             "partial_plus_reduce_avg_us": round(tot_ms / max(calls, 1) * 1e3, 3),
         },
