@@ -35,6 +35,8 @@ def parse():
     ap.add_argument("--config", default="M0", help="workload name (decode: M0, C1..C5; KV write: W0..W2)")
     ap.add_argument("--sets", type=int, default=0, help="input sets to rotate (0: enough for >1 GB)")
     ap.add_argument("--chunk", type=int, default=0, help="split size in tokens (0: library default)")
+    ap.add_argument("--block-scores", action="store_true",
+                    help="also compute the pooled 128-token block scores in each step")
     ap.add_argument("--graph", action="store_true",
                     help="replay each decode step from a captured HIP graph (no per-step host work)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
@@ -273,13 +275,13 @@ def main():
 
     if args.graph:
         from fasterkernels_amd.graph import DecodeGraph
-        graphs = [DecodeGraph(W.run, s, chunk_tokens=args.chunk) for s in sets]
+        graphs = [DecodeGraph(W.run, s, chunk_tokens=args.chunk, block_scores=args.block_scores) for s in sets]
 
         def step(i):
             return graphs[i % n_sets].replay()
     else:
         def step(i):
-            return W.run(sets[i % n_sets], chunk_tokens=args.chunk)
+            return W.run(sets[i % n_sets], chunk_tokens=args.chunk, block_scores=args.block_scores)
 
     for i in range(args.warmup):
         step(i)
@@ -319,7 +321,8 @@ def main():
     if args.graph:   # the replay (partial + reduce) is the timed unit
         part_avg_ms = tot_ms / max(calls, 1)
     kern_gbs = alg_bytes / (part_avg_ms / 1e3) / 1e9 if part_avg_ms > 0 else None
-    traffic = read_traffic(args.traffic) if args.config == "M0" and not args.chunk and not args.graph else None
+    traffic = (read_traffic(args.traffic) if args.config == "M0" and not (args.chunk or args.graph or args.block_scores)
+               else None)
 
     out = {
         "metric": METRIC,
@@ -342,6 +345,7 @@ def main():
             "batch": base.B, "total_tokens": base.total_tokens, "algorithmic_bytes": alg_bytes,
             "chunk_tokens": args.chunk or "auto",
             "launch": "hip graph replay" if args.graph else "eager",
+            "block_scores": bool(args.block_scores),
         },
         "roofline": {
             "bound": "hbm",

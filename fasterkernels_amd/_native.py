@@ -50,6 +50,12 @@ SIGNATURES = {
                               _I, _P]),
     "fsk_decode_dense": (_I, [_P, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _L, _P, _P, _P, _I, _P,
                               _P, _P, _P, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _P, _L, _I, _P]),
+    "fsk_score_workspace_bytes": (_L, [_I, _I, _I]),
+    "fsk_decode_varlen_scores": (_I, [_P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P, _P,
+                                      _P, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _P, _L, _I, _P, _I, _P]),
+    "fsk_decode_paged_scores": (_I, [_P, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _I, _P, _I, _I,
+                                     _P, _I, _P, _P, _P, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _P, _L,
+                                     _I, _P, _I, _P]),
     "fsk_paged_gather": (_I, [_P, _L, _L, _L, _P, _L, _I, _P, _I, _I, _I, _I, _I, _I, _P, _P]),
     "fsk_paged_write": (_I, [_P, _L, _L, _P, _L, _L, _P, _L, _P, _L, _L, _L, _P, _L, _L, _L, _I, _I,
                              _I, _I, _I, _I, _P, _P, _P, _L, _P, _L, _P]),
@@ -108,6 +114,13 @@ def set_option(name: str, value: int) -> None:
 def workspace_bytes(layout: int, batch: int, hq: int, hkv: int, d: int, kv_extent: int,
                     page_size: int = 16, chunk_tokens: int = 0) -> int:
     n = load().fsk_workspace_bytes(layout, batch, hq, hkv, d, kv_extent, page_size, chunk_tokens)
+    if n < 0:
+        check(int(n))
+    return int(n)
+
+
+def score_workspace_bytes(batch: int, hq: int, score_blocks: int) -> int:
+    n = load().fsk_score_workspace_bytes(batch, hq, score_blocks)
     if n < 0:
         check(int(n))
     return int(n)

@@ -186,6 +186,11 @@ struct Params {
   int32_t* plan;           // [B+1] unit prefix offsets
   float* part_ml;          // [u_max, Hkv, G, 2]
   float* part_acc;         // [u_max, Hkv, G, D]
+  // Block scores (kScores kernels only): raw log2-domain maximum of each
+  // 128-token block [B, Hq, nblk] and the sequence lengths [B] for the reduce.
+  float* blk_max;
+  int32_t* lens_out;
+  int nblk;
 };
 
 // Token range [start, start+len) of sequence b in its layout's row space.
@@ -252,8 +257,10 @@ __device__ __forceinline__ HalfTile half_tile(const Params& p, int b, int start,
 // clamped to [chunk_min, chunk_max]; the host sizes u_max for chunk_max, so
 // the table always fits.  Workgroup 0 publishes the table for the reduce
 // kernel.  Every workgroup computes the same result from the same lengths.
-template <int kLayout>
+template <int kLayout, bool kScores>
 __device__ int build_plan(const Params& p, int32_t* pre, int& chunk_out) {
+  // Split sizes are multiples of 32 tokens (one tile), of 128 with block scores.
+  constexpr int kAlign = kScores ? 128 : 32;
   const int lane = threadIdx.x;
   // Lengths of sequences lane, lane + 64, ...; the first block stays in a
   // register so that the common case (B <= 64) reads them once.
@@ -280,7 +287,7 @@ __device__ int build_plan(const Params& p, int32_t* pre, int& chunk_out) {
   int64_t want = (total + p.target_units - 1) / p.target_units;
   if (p.u_max > p.B) want = std::max<int64_t>(want, (total + (p.u_max - p.B) - 1) / (p.u_max - p.B));
   else want = p.chunk_max;
-  want = (want + 31) / 32 * 32;
+  want = (want + kAlign - 1) / kAlign * kAlign;
   const int chunk = uniform((int)std::min<int64_t>(std::max<int64_t>(want, p.chunk_min), p.chunk_max));
   chunk_out = chunk;
 
@@ -303,6 +310,8 @@ __device__ int build_plan(const Params& p, int32_t* pre, int& chunk_out) {
       if (lane >= off) incl += y;
     }
     if (b < p.B) pre[b] = min(carry + incl - n, p.u_max);
+    if constexpr (kScores)
+      if (blockIdx.x == 0 && b < p.B) p.lens_out[b] = len;
     carry += __shfl(incl, kWave - 1, kWave);
   }
   const int total_units = min(carry, p.u_max);
@@ -430,9 +439,11 @@ struct Softmax {
   f32x4 acc[kDpc];
 };
 
+// Returns the tile's maximum score of head column c (log2 domain, -inf when
+// the tile has no valid row).
 template <int D, int kQ, int kKV>
-__device__ __forceinline__ void compute_tile(const TileRegs<D, kKV>& T, Softmax<D, kQ, kKV>& st,
-                                             const u32x4 (&qop)[D / 32], float sscale, int g) {
+__device__ __forceinline__ float compute_tile(const TileRegs<D, kKV>& T, Softmax<D, kQ, kKV>& st,
+                                              const u32x4 (&qop)[D / 32], float sscale, int g) {
   using TR = TileRegs<D, kKV>;
   using SM = Softmax<D, kQ, kKV>;
   constexpr int kSteps = SM::kSteps;
@@ -534,7 +545,26 @@ __device__ __forceinline__ void compute_tile(const TileRegs<D, kKV>& T, Softmax<
     st.acc[j] = mfma16x16x32<SM::kPvBf16>(vop, pop, st.acc[j]);
     if constexpr (SM::kPvBf16) st.acc[j] = mfma16x16x32<true>(vop, plo, st.acc[j]);
   }
+  return mt;
 }
+
+// Block scores: running maximum of the current 128-token block, stored when
+// the block (or the unit) ends.  Units start on block boundaries (the split
+// size is a multiple of 128 when scores are requested).
+constexpr int kScoreBlock = 128;
+struct BlockMax {
+  float m = -INFINITY;
+  __device__ __forceinline__ void add(const Params& p, const Unit& un, int t, float mt, int head, bool head_ok,
+                                      int g) {
+    m = fmaxf(m, mt);
+    if (((t + 32) % kScoreBlock) == 0 || t + 32 >= un.t_end) {
+      const int blk = t / kScoreBlock;
+      if (head_ok && g == 0 && blk < p.nblk)
+        p.blk_max[((int64_t)un.b * p.Hkv * p.G + un.kvh * p.G + head) * p.nblk + blk] = m;
+      m = -INFINITY;
+    }
+  }
+};
 
 #ifndef FSK_PIPE_DEPTH
 #define FSK_PIPE_DEPTH 2
@@ -542,7 +572,7 @@ __device__ __forceinline__ void compute_tile(const TileRegs<D, kKV>& T, Softmax<
 // Waves per SIMD the register budget is sized for (2: <= 256 VGPRs).
 constexpr int kWavesPerEu = FSK_PIPE_DEPTH > 2 ? 1 : 2;
 
-template <int D, int kQ, int kKV, int kLayout>
+template <int D, int kQ, int kKV, int kLayout, bool kScores>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu))) void partial_kernel(Params p) {
   using TR = TileRegs<D, kKV>;
   using SM = Softmax<D, kQ, kKV>;
@@ -560,7 +590,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   const int c = lane & 15;
 
   int chunk;
-  const int total_units = build_plan<kLayout>(p, s_pre, chunk);
+  const int total_units = build_plan<kLayout, kScores>(p, s_pre, chunk);
   const int NH = p.Hkv * p.n_hb;
   const int64_t W = (int64_t)total_units * NH;
   const float k_scale = kKvFp8 ? p.k_scale[0] : 1.0f;
@@ -626,6 +656,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     st.l_run = 0.f;
 #pragma unroll
     for (int j = 0; j < kDpc; ++j) st.acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    BlockMax bm;
 
     if constexpr (kDepth > 1) {
       // Tile slot s holds tile n with n % kDepth == s; while tile n is
@@ -642,7 +673,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
           if (!done) {
             const int tn = t + 32 * (kDepth - 1);
             if (tn < un.t_end) issue_tile<D, kKV, kLayout>(tiles[(s + kDepth - 1) % kDepth], p, un, tn, g, c);
-            compute_tile<D, kQ, kKV>(tiles[s], st, qop, sscale, g);
+            const float mt = compute_tile<D, kQ, kKV>(tiles[s], st, qop, sscale, g);
+            if constexpr (kScores) bm.add(p, un, t, mt, head, head_ok, g);
             t += 32;
             done = t >= un.t_end;
           }
@@ -652,7 +684,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
       TR ta;
       for (int t = un.t_begin; t < un.t_end; t += 32) {
         issue_tile<D, kKV, kLayout>(ta, p, un, t, g, c);
-        compute_tile<D, kQ, kKV>(ta, st, qop, sscale, g);
+        const float mt = compute_tile<D, kQ, kKV>(ta, st, qop, sscale, g);
+        if constexpr (kScores) bm.add(p, un, t, mt, head, head_ok, g);
       }
     }
 
@@ -686,6 +719,12 @@ struct ReduceParams {
   uint8_t* out;
   int64_t o_sb, o_sh;  // bytes
   int Hq, Hkv, G;
+  // Block scores (null scores: none): S[b, h, j] = largest attention
+  // probability of block j = exp2(blk_max - M) / den; 0 past the sequence.
+  const float* blk_max;
+  const int32_t* lens;
+  uint8_t* scores;     // [B, Hq, nblk] in the output dtype, contiguous
+  int nblk;
 };
 
 constexpr int kReduceThreads = 256;
@@ -765,6 +804,7 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) 
     den += s_l[q];
   }
 
+  float ref = M_use;  // reference point of den
   if (p.s_aux) {
     const float z = p.s_aux[h];
     if (p.sink_mode == FSK_SINK_EXP) {
@@ -776,8 +816,22 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) 
       const float fs = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - Mn_use);
       den = den * fs + __builtin_amdgcn_exp2f(z2 - Mn_use);
       num *= fs;
+      ref = Mn_use;
     } else {
       den += z;  // linear fold relative to the running max (flash_decode_cuda.cu:151-153)
+    }
+  }
+
+  if (p.scores) {
+    const int nvalid = (p.lens[b] + kScoreBlock - 1) / kScoreBlock;
+    const float inv = 1.f / den;
+    const float* src = p.blk_max + ((int64_t)b * p.Hq + h) * p.nblk;
+    uint8_t* dst = p.scores + ((int64_t)b * p.Hq + h) * p.nblk * (kOut == kF32 ? 4 : 2);
+    for (int j = d4; j < p.nblk; j += kD4) {
+      const float sc = j < nvalid ? __builtin_amdgcn_exp2f(src[j] - ref) * inv : 0.f;
+      if constexpr (kOut == kF32) ((float*)dst)[j] = sc;
+      else if constexpr (kOut == kF16) ((f16*)dst)[j] = (f16)sc;
+      else ((bf16*)dst)[j] = (bf16)sc;
     }
   }
 
@@ -1168,9 +1222,15 @@ struct Common {
   float sm_scale;
   void* ws; int64_t ws_bytes; int chunk;
   hipStream_t stream;
+  void* scores; int nblk;  // block scores [B, Hq, nblk] in the output dtype, or null
 };
 
 bool aligned(const void* p, int a) { return ((uintptr_t)p % a) == 0; }
+
+// Extra workspace of a call with block scores: raw block maxima + lengths.
+int64_t score_ws_bytes(int B, int Hq, int nblk) {
+  return align256((int64_t)B * Hq * nblk * 4) + align256(4 * (int64_t)B);
+}
 
 int validate(const Common& c) {
   if (c.B < 0 || c.Hq <= 0 || c.Hkv <= 0) return fail(FSK_ERR_INVALID, "batch/heads must be positive");
@@ -1213,30 +1273,40 @@ int validate(const Common& c) {
     if ((int64_t)c.max_blocks * c.page_size >= ((int64_t)1 << 31)) return fail(FSK_ERR_UNSUPPORTED, "block table too wide");
   }
   if (c.B > 16384) return fail(FSK_ERR_UNSUPPORTED, "batch above 16384");
+  if (c.scores) {
+    if (c.layout == FSK_LAYOUT_DENSE) return fail(FSK_ERR_UNSUPPORTED, "block scores on the varlen and paged layouts only");
+    if (c.nblk <= 0 || c.nblk > (1 << 24)) return fail(FSK_ERR_INVALID, "score_blocks must be in [1, 2^24]");
+    if (!aligned(c.scores, elem_bytes(c.o_dt))) return fail(FSK_ERR_INVALID, "scores must be aligned to the output dtype");
+    if (c.chunk % 128) return fail(FSK_ERR_INVALID, "with block scores chunk_tokens must be 0 or a multiple of 128");
+  }
   return FSK_OK;
 }
 
-template <int D, int kQ, int kKV, int kLayout>
+template <int D, int kQ, int kKV, int kLayout, bool kScores>
 void launch_partial(const Params& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((partial_kernel<D, kQ, kKV, kLayout>), dim3(grid), dim3(64), 4 * (p.B + 1), s, p);
+  hipLaunchKernelGGL((partial_kernel<D, kQ, kKV, kLayout, kScores>), dim3(grid), dim3(64), 4 * (p.B + 1), s, p);
 }
 
-template <int D, int kLayout>
+template <int D, int kLayout, bool kScores>
 int dispatch_qkv(const Params& p, int grid, int q_dt, int kv_dt, hipStream_t s) {
-  if (kv_dt == FSK_F16) launch_partial<D, kF16, kF16, kLayout>(p, grid, s);
-  else if (kv_dt == FSK_BF16) launch_partial<D, kBF16, kBF16, kLayout>(p, grid, s);
-  else if (q_dt == FSK_F16) launch_partial<D, kF16, kE4M3, kLayout>(p, grid, s);
-  else if (q_dt == FSK_BF16) launch_partial<D, kBF16, kE4M3, kLayout>(p, grid, s);
-  else if constexpr (kLayout == kDense) launch_partial<D, kE4M3, kE4M3, kLayout>(p, grid, s);
+  if (kv_dt == FSK_F16) launch_partial<D, kF16, kF16, kLayout, kScores>(p, grid, s);
+  else if (kv_dt == FSK_BF16) launch_partial<D, kBF16, kBF16, kLayout, kScores>(p, grid, s);
+  else if (q_dt == FSK_F16) launch_partial<D, kF16, kE4M3, kLayout, kScores>(p, grid, s);
+  else if (q_dt == FSK_BF16) launch_partial<D, kBF16, kE4M3, kLayout, kScores>(p, grid, s);
+  else if constexpr (kLayout == kDense) launch_partial<D, kE4M3, kE4M3, kLayout, kScores>(p, grid, s);
   else return fail(FSK_ERR_UNSUPPORTED, "e4m3 q only on the dense layout");
   return FSK_OK;
 }
 
 template <int D>
-int dispatch_layout(int layout, const Params& p, int grid, int q_dt, int kv_dt, hipStream_t s) {
-  if (layout == FSK_LAYOUT_VARLEN) return dispatch_qkv<D, kVarlen>(p, grid, q_dt, kv_dt, s);
-  if (layout == FSK_LAYOUT_PAGED) return dispatch_qkv<D, kPaged>(p, grid, q_dt, kv_dt, s);
-  return dispatch_qkv<D, kDense>(p, grid, q_dt, kv_dt, s);
+int dispatch_layout(int layout, bool scores, const Params& p, int grid, int q_dt, int kv_dt, hipStream_t s) {
+  if (layout == FSK_LAYOUT_VARLEN)
+    return scores ? dispatch_qkv<D, kVarlen, true>(p, grid, q_dt, kv_dt, s)
+                  : dispatch_qkv<D, kVarlen, false>(p, grid, q_dt, kv_dt, s);
+  if (layout == FSK_LAYOUT_PAGED)
+    return scores ? dispatch_qkv<D, kPaged, true>(p, grid, q_dt, kv_dt, s)
+                  : dispatch_qkv<D, kPaged, false>(p, grid, q_dt, kv_dt, s);
+  return dispatch_qkv<D, kDense, false>(p, grid, q_dt, kv_dt, s);
 }
 
 template <int D>
@@ -1262,8 +1332,11 @@ int run_decode(const Common& c) {
   const int64_t u_max = sp.u_max;
   if (u_max >= ((int64_t)1 << 31) / (c.Hkv * (int64_t)n_hb)) return fail(FSK_ERR_UNSUPPORTED, "too many work units");
   const WsLayout wl = ws_layout(c.B, c.Hkv, G, c.D, u_max);
-  if (!c.ws || c.ws_bytes < wl.total || !aligned(c.ws, 256))
-    return fail(FSK_ERR_WORKSPACE, "workspace missing, unaligned or smaller than fsk_workspace_bytes()");
+  const int64_t need = wl.total + (c.scores ? score_ws_bytes(c.B, c.Hq, c.nblk) : 0);
+  if (!c.ws || c.ws_bytes < need || !aligned(c.ws, 256))
+    return fail(FSK_ERR_WORKSPACE, c.scores ? "workspace missing, unaligned or smaller than fsk_workspace_bytes() + "
+                                              "fsk_score_workspace_bytes()"
+                                            : "workspace missing, unaligned or smaller than fsk_workspace_bytes()");
 
   const int qe = elem_bytes(c.q_dt), ke = elem_bytes(c.kv_dt), oe = elem_bytes(c.o_dt);
   Params p;
@@ -1286,6 +1359,11 @@ int run_decode(const Common& c) {
   p.plan = (int32_t*)(ws + wl.plan_off);
   p.part_ml = (float*)(ws + wl.ml_off);
   p.part_acc = (float*)(ws + wl.acc_off);
+  if (c.scores) {
+    p.nblk = c.nblk;
+    p.blk_max = (float*)(ws + wl.total);
+    p.lens_out = (int32_t*)(ws + wl.total + align256((int64_t)c.B * c.Hq * c.nblk * 4));
+  }
 
   const int64_t w_max = u_max * c.Hkv * n_hb;
   const int64_t grid64 = std::min<int64_t>(w_max, (int64_t)cus * g_opt.waves_per_cu);
@@ -1295,9 +1373,10 @@ int run_decode(const Common& c) {
   const bool rec = timing_this_call();
   timing_mark(rec, c.stream);
   int rc;
-  if (c.D == 64) rc = dispatch_layout<64>(c.layout, p, grid, c.q_dt, c.kv_dt, c.stream);
-  else if (c.D == 128) rc = dispatch_layout<128>(c.layout, p, grid, c.q_dt, c.kv_dt, c.stream);
-  else rc = dispatch_layout<256>(c.layout, p, grid, c.q_dt, c.kv_dt, c.stream);
+  const bool sc = c.scores != nullptr;
+  if (c.D == 64) rc = dispatch_layout<64>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, c.stream);
+  else if (c.D == 128) rc = dispatch_layout<128>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, c.stream);
+  else rc = dispatch_layout<256>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, c.stream);
   if (rc != FSK_OK) {
     if (rec && g_timing.enabled && !g_timing.ev.empty()) {  // drop this call's first mark
       g_timing.spare.push_back(g_timing.ev.back());
@@ -1312,6 +1391,7 @@ int run_decode(const Common& c) {
   rp.s_aux = c.s_aux; rp.sink_mode = c.sink_mode;
   rp.out = (uint8_t*)c.out; rp.o_sb = c.o_sb * oe; rp.o_sh = c.o_sh * oe;
   rp.Hq = c.Hq; rp.Hkv = c.Hkv; rp.G = G;
+  rp.blk_max = p.blk_max; rp.lens = p.lens_out; rp.scores = (uint8_t*)c.scores; rp.nblk = c.nblk;
   if (c.D == 64) launch_reduce<64>(rp, c.B, c.o_dt, c.stream);
   else if (c.D == 128) launch_reduce<128>(rp, c.B, c.o_dt, c.stream);
   else launch_reduce<256>(rp, c.B, c.o_dt, c.stream);
@@ -1493,6 +1573,64 @@ int64_t fsk_workspace_bytes(int layout, int batch, int num_q_heads, int num_kv_h
   const SplitPlan sp = plan_split(layout, B, num_kv_heads, n_hb, kv_extent, page_size, chunk_tokens, device_cus());
   const int64_t u_max = sp.u_max;
   return ws_layout(B, num_kv_heads, G, head_dim, u_max).total;
+}
+
+int64_t fsk_score_workspace_bytes(int batch, int num_q_heads, int score_blocks) {
+  if (batch < 0 || num_q_heads <= 0 || score_blocks <= 0 || score_blocks > (1 << 24))
+    return fail(FSK_ERR_INVALID, "bad shape");
+  return score_ws_bytes(batch > 0 ? batch : 1, num_q_heads, score_blocks);
+}
+
+int fsk_decode_varlen_scores(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
+                             int64_t k_stride_t, int64_t k_stride_h, const void* v, int64_t v_stride_t,
+                             int64_t v_stride_h, const int32_t* cu_seqlens, int64_t total_tokens, const float* s_aux,
+                             int sink_mode, const float* k_scale, const float* v_scale, void* out,
+                             int64_t o_stride_b, int64_t o_stride_h, int batch, int num_q_heads, int num_kv_heads,
+                             int head_dim, int q_dtype, int kv_dtype, int out_dtype, float sm_scale,
+                             void* workspace, int64_t workspace_bytes, int chunk_tokens, void* scores,
+                             int score_blocks, void* stream) {
+  if (!scores) return fail(FSK_ERR_INVALID, "null scores");
+  Common c;
+  memset(&c, 0, sizeof(c));
+  c.layout = FSK_LAYOUT_VARLEN;
+  c.q = q; c.q_sb = q_stride_b; c.q_sh = q_stride_h;
+  c.k = k; c.k_st = k_stride_t; c.k_sh = k_stride_h;
+  c.v = v; c.v_st = v_stride_t; c.v_sh = v_stride_h;
+  c.lens = cu_seqlens; c.kv_extent = total_tokens;
+  c.s_aux = s_aux; c.sink_mode = sink_mode; c.k_scale = k_scale; c.v_scale = v_scale;
+  c.out = out; c.o_sb = o_stride_b; c.o_sh = o_stride_h;
+  c.B = batch; c.Hq = num_q_heads; c.Hkv = num_kv_heads; c.D = head_dim;
+  c.q_dt = q_dtype; c.kv_dt = kv_dtype; c.o_dt = out_dtype; c.sm_scale = sm_scale;
+  c.ws = workspace; c.ws_bytes = workspace_bytes; c.chunk = chunk_tokens; c.stream = (hipStream_t)stream;
+  c.scores = scores; c.nblk = score_blocks;
+  return run_decode(c);
+}
+
+int fsk_decode_paged_scores(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_pool,
+                            int64_t k_stride_p, int64_t k_stride_h, int64_t k_stride_t, const void* v_pool,
+                            int64_t v_stride_p, int64_t v_stride_h, int64_t v_stride_t, const int32_t* block_table,
+                            int64_t bt_stride_b, int max_blocks, const int32_t* seq_lens, int num_pages,
+                            int page_size, const float* s_aux, int sink_mode, const float* k_scale,
+                            const float* v_scale, void* out, int64_t o_stride_b, int64_t o_stride_h, int batch,
+                            int num_q_heads, int num_kv_heads, int head_dim, int q_dtype, int kv_dtype,
+                            int out_dtype, float sm_scale, void* workspace, int64_t workspace_bytes,
+                            int chunk_tokens, void* scores, int score_blocks, void* stream) {
+  if (!scores) return fail(FSK_ERR_INVALID, "null scores");
+  Common c;
+  memset(&c, 0, sizeof(c));
+  c.layout = FSK_LAYOUT_PAGED;
+  c.q = q; c.q_sb = q_stride_b; c.q_sh = q_stride_h;
+  c.k = k_pool; c.k_s0 = k_stride_p; c.k_sh = k_stride_h; c.k_st = k_stride_t;
+  c.v = v_pool; c.v_s0 = v_stride_p; c.v_sh = v_stride_h; c.v_st = v_stride_t;
+  c.bt = block_table; c.bt_sb = bt_stride_b; c.max_blocks = max_blocks;
+  c.lens = seq_lens; c.num_pages = num_pages; c.page_size = page_size; c.kv_extent = max_blocks;
+  c.s_aux = s_aux; c.sink_mode = sink_mode; c.k_scale = k_scale; c.v_scale = v_scale;
+  c.out = out; c.o_sb = o_stride_b; c.o_sh = o_stride_h;
+  c.B = batch; c.Hq = num_q_heads; c.Hkv = num_kv_heads; c.D = head_dim;
+  c.q_dt = q_dtype; c.kv_dt = kv_dtype; c.o_dt = out_dtype; c.sm_scale = sm_scale;
+  c.ws = workspace; c.ws_bytes = workspace_bytes; c.chunk = chunk_tokens; c.stream = (hipStream_t)stream;
+  c.scores = scores; c.nblk = score_blocks;
+  return run_decode(c);
 }
 
 int fsk_decode_varlen(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k, int64_t k_stride_t,

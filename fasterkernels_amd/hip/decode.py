@@ -137,7 +137,8 @@ def _check_q(q: torch.Tensor):
 def flash_decode_gqa_varlen(q, k_varlen, v_varlen, cu_seqlens_k, s_aux=None, *,
                             sink_mode: str = "exp", k_scale=None, v_scale=None,
                             out_dtype: torch.dtype | None = None, sm_scale: float | None = None,
-                            chunk_tokens: int = 0):
+                            chunk_tokens: int = 0, return_block_scores: bool = False,
+                            score_blocks: int | None = None):
     """Varlen GQA flash decode: out[b, h] = softmax(q[b,h] . K_b^T * sm_scale) V_b.
 
     Reference: fskernels/triton/triton_gqa_decode.py:126-155 (and the positional
@@ -148,6 +149,12 @@ def flash_decode_gqa_varlen(q, k_varlen, v_varlen, cu_seqlens_k, s_aux=None, *,
     reference tests' oracle; "linear": added to the denominator as the
     reference kernels do).  Returns a new [B, Hq, D] tensor of q's dtype
     (``out_dtype`` overrides it).  fp8 K/V need k_scale / v_scale.
+
+    ``return_block_scores=True`` returns ``(out, S)`` with S [B, Hq, n] the
+    largest attention probability of each 128-token block of each sequence
+    (0 past its end), the S output of the TileLang kernel
+    (fskernels/tilelang/tilelang_gqa_decode.py:123-130); n = ``score_blocks``
+    or enough blocks for total_tokens.
     """
     q = _check_q(q)
     dev = q.device
@@ -171,20 +178,35 @@ def flash_decode_gqa_varlen(q, k_varlen, v_varlen, cu_seqlens_k, s_aux=None, *,
     out = torch.empty((B, Hq, D), dtype=odt, device=dev)
     scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
     nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_VARLEN, B, Hq, Hkv, D, T, 16, chunk_tokens)
+    scores, nblk = _scores_out(return_block_scores, score_blocks, T, B, Hq, odt, dev)
+    if scores is not None:
+        nbytes += nat.score_workspace_bytes(B, Hq, nblk)
     ws = _workspace(nbytes, dev)
     lib = nat.load()
-    with torch.cuda.device(dev):
-        st = lib.fsk_decode_varlen(
-            q.data_ptr(), q.stride(0), q.stride(1),
+    args = (q.data_ptr(), q.stride(0), q.stride(1),
             k.data_ptr(), k.stride(0), k.stride(1),
             v.data_ptr(), v.stride(0), v.stride(1),
             cu.data_ptr(), T, nat.ptr(sinks), _sink_mode(sink_mode), ksp, vsp,
             out.data_ptr(), out.stride(0), out.stride(1),
             B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_varlen"),
-            _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens,
-            nat.stream_handle(dev))
+            _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens)
+    with torch.cuda.device(dev):
+        if scores is None:
+            st = lib.fsk_decode_varlen(*args, nat.stream_handle(dev))
+        else:
+            st = lib.fsk_decode_varlen_scores(*args, scores.data_ptr(), nblk, nat.stream_handle(dev))
     nat.check(st)
-    return out
+    return out if scores is None else (out, scores)
+
+
+def _scores_out(wanted, score_blocks, extent_tokens, B, Hq, odt, dev):
+    """Block-score output [B, Hq, n] (n = score_blocks or ceil(extent / 128)), or (None, 0)."""
+    if not wanted:
+        return None, 0
+    n = int(score_blocks) if score_blocks is not None else max(1, -(-int(extent_tokens) // 128))
+    if n <= 0:
+        raise ValueError("score_blocks must be positive")
+    return torch.empty((B, Hq, n), dtype=odt, device=dev), n
 
 
 # ---------------------------------------------------------------------------
@@ -274,7 +296,8 @@ def flash_decode_gqa_hf_fp8(q_fp8, k_cache_fp8, v_cache_fp8, cache_lens, scale_q
 def paged_flash_decode(q, k_pool, v_pool, block_table, seq_lens, page_size, *, s_aux=None,
                        k_scale=None, v_scale=None, out_dtype: torch.dtype | None = None,
                        sink_mode: str = "exp", sm_scale: float | None = None,
-                       chunk_tokens: int = 0):
+                       chunk_tokens: int = 0, return_block_scores: bool = False,
+                       score_blocks: int | None = None):
     """Paged GQA decode through a block table.
 
     Reference: fskernels/paged_attn/triton_paged_attn.py:96-125.  q [B, Hq, D];
@@ -282,7 +305,8 @@ def paged_flash_decode(q, k_pool, v_pool, block_table, seq_lens, page_size, *, s
     block_table int32 [B, max_blocks] (logical page -> physical page, entries
     past a sequence's last page are never read); seq_lens int32 [B].  The
     keyword-only arguments add sinks and fp8 (e4m3) pools with per-tensor
-    scales, which the reference kernel does not have.
+    scales, which the reference kernel does not have, and the block scores of
+    flash_decode_gqa_varlen (default width: the block table's token capacity).
     """
     q = _check_q(q)
     dev = q.device
@@ -315,21 +339,26 @@ def paged_flash_decode(q, k_pool, v_pool, block_table, seq_lens, page_size, *, s
     scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
     max_blocks = bt.shape[1]
     nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_PAGED, B, Hq, Hkv, D, max_blocks, PS, chunk_tokens)
+    scores, nblk = _scores_out(return_block_scores, score_blocks, max_blocks * PS, B, Hq, odt, dev)
+    if scores is not None:
+        nbytes += nat.score_workspace_bytes(B, Hq, nblk)
     ws = _workspace(nbytes, dev)
     lib = nat.load()
-    with torch.cuda.device(dev):
-        st = lib.fsk_decode_paged(
-            q.data_ptr(), q.stride(0), q.stride(1),
+    args = (q.data_ptr(), q.stride(0), q.stride(1),
             k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
             v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
             bt.data_ptr(), bt.stride(0), max_blocks, lens.data_ptr(), P, PS,
             nat.ptr(sinks), _sink_mode(sink_mode), ksp, vsp,
             out.data_ptr(), out.stride(0), out.stride(1),
             B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_pool"),
-            _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens,
-            nat.stream_handle(dev))
+            _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens)
+    with torch.cuda.device(dev):
+        if scores is None:
+            st = lib.fsk_decode_paged(*args, nat.stream_handle(dev))
+        else:
+            st = lib.fsk_decode_paged_scores(*args, scores.data_ptr(), nblk, nat.stream_handle(dev))
     nat.check(st)
-    return out
+    return out if scores is None else (out, scores)
 
 
 # ---------------------------------------------------------------------------

@@ -186,17 +186,19 @@ def make(name: str = "M0", *, device=None, seed: int | None = None, overrides: d
     return wl.to(device) if device is not None else wl
 
 
-def run(wl: Workload, *, sink_mode: str = "exp", chunk_tokens: int = 0):
-    """One decode step of ``wl`` through the HIP entry points."""
+def run(wl: Workload, *, sink_mode: str = "exp", chunk_tokens: int = 0, block_scores: bool = False):
+    """One decode step of ``wl`` through the HIP entry points (with
+    ``block_scores``: also the pooled block scores, returned as (out, S))."""
     from .hip import decode as dec
     if wl.layout == "paged":
         return dec.paged_flash_decode(wl.q, wl.k, wl.v, wl.block_table, wl.seq_lens, PAGE,
                                       s_aux=wl.s_aux, k_scale=wl.k_scale, v_scale=wl.v_scale,
                                       out_dtype=wl.out_dtype, sink_mode=sink_mode,
-                                      chunk_tokens=chunk_tokens)
+                                      chunk_tokens=chunk_tokens, return_block_scores=block_scores)
     return dec.flash_decode_gqa_varlen(wl.q, wl.k, wl.v, wl.cu_seqlens, wl.s_aux,
                                        sink_mode=sink_mode, k_scale=wl.k_scale, v_scale=wl.v_scale,
-                                       out_dtype=wl.out_dtype, chunk_tokens=chunk_tokens)
+                                       out_dtype=wl.out_dtype, chunk_tokens=chunk_tokens,
+                                       return_block_scores=block_scores)
 
 
 # ---------------------------------------------------------------------------

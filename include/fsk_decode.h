@@ -126,6 +126,47 @@ FSK_API int fsk_decode_paged(const void *q, int64_t q_stride_b, int64_t q_stride
                      void *workspace, int64_t workspace_bytes, int chunk_tokens,
                      void *stream);
 
+/* Block scores: the varlen / paged decode plus, per sequence b, query head h
+ * and 128-token block j of the sequence, the largest final attention
+ * probability of a token of that block:
+ *   S[b, h, j] = max_{t in [128 j, 128 j + 128) and t < len_b} p_t,
+ * p_t = softmax weight of token t (the sink folded into the denominator as
+ * sink_mode says); S = 0 for blocks at or past the sequence end.
+ * Replaces: the S output of fskernels/tilelang/tilelang_gqa_decode.py:40-132
+ *           (block maxima :102-103, normalised :123-124, stored :129-130),
+ *           which that module's flash_decode_gqa_varlen computes and drops (:170).
+ * scores: [B, Hq, score_blocks] contiguous, in out_dtype; blocks past
+ * score_blocks are not stored.  The workspace must hold
+ * fsk_workspace_bytes(...) + fsk_score_workspace_bytes(B, Hq, score_blocks)
+ * bytes, and a fixed chunk_tokens must be a multiple of 128.  Other
+ * arguments as fsk_decode_varlen / fsk_decode_paged. */
+FSK_API int64_t fsk_score_workspace_bytes(int batch, int num_q_heads, int score_blocks);
+FSK_API int fsk_decode_varlen_scores(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                      const void *k, int64_t k_stride_t, int64_t k_stride_h,
+                      const void *v, int64_t v_stride_t, int64_t v_stride_h,
+                      const int32_t *cu_seqlens, int64_t total_tokens,
+                      const float *s_aux, int sink_mode,
+                      const float *k_scale, const float *v_scale,
+                      void *out, int64_t o_stride_b, int64_t o_stride_h,
+                      int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                      int q_dtype, int kv_dtype, int out_dtype, float sm_scale,
+                      void *workspace, int64_t workspace_bytes, int chunk_tokens,
+                      void *scores, int score_blocks, void *stream);
+FSK_API int fsk_decode_paged_scores(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                     const void *k_pool, int64_t k_stride_p, int64_t k_stride_h,
+                     int64_t k_stride_t,
+                     const void *v_pool, int64_t v_stride_p, int64_t v_stride_h,
+                     int64_t v_stride_t,
+                     const int32_t *block_table, int64_t bt_stride_b, int max_blocks,
+                     const int32_t *seq_lens, int num_pages, int page_size,
+                     const float *s_aux, int sink_mode,
+                     const float *k_scale, const float *v_scale,
+                     void *out, int64_t o_stride_b, int64_t o_stride_h,
+                     int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                     int q_dtype, int kv_dtype, int out_dtype, float sm_scale,
+                     void *workspace, int64_t workspace_bytes, int chunk_tokens,
+                     void *scores, int score_blocks, void *stream);
+
 /* Dense (HF static cache) GQA decode.
  * Replaces: fskernels/triton/triton_gqa_decode_hf.py:146-211
  *           (flash_decode_gqa_hf_dense_optimized: partial :186-199 + reduce

@@ -27,6 +27,8 @@ It restates, in plain numpy, what the reference computes on the decode path:
   k[b, h, :, :] (fskernels/triton/triton_gqa_decode_hf.py:46-54, :62-64).
 * Split-KV partials and their log-sum-exp merge
   (triton_gqa_decode_hf.py:52-54, :90-99, :103-137).
+* Pooled block scores (the TileLang kernel's S output): the largest
+  attention probability within each 128-token block.
 * The KV write path: PagedKVCache's page bookkeeping and row stores
   (fskernels/paged_attn/paged_kv_cache.py:44-141) restated as
   RefPagedKVCache, and the slot-addressed batch store paged_write with the
@@ -210,6 +212,70 @@ def decode_dense(q, k, v, cache_lens, start_offsets=None, s_aux=None, sink_mode=
         if v_scale is not None:
             vb = dequantize_fp8(vb, v_scale)
         outs.append(attend(q[b], kb, vb, s_aux, sink_mode, sm_scale))
+    return np.stack(outs)
+
+
+# ---------------------------------------------------------------------------
+# pooled block scores
+# ---------------------------------------------------------------------------
+SCORE_BLOCK = 128
+
+
+def block_scores(q, k, sink=None, sink_mode: str = "exp", sm_scale=None, n_blocks=None,
+                 block: int = SCORE_BLOCK):
+    """[Hq, n_blocks]: for each 128-token block of one sequence, the largest
+    final attention probability of its tokens (0 for blocks past the end).
+
+    Restates the S output of fskernels/tilelang/tilelang_gqa_decode.py:
+    block maxima of the scores (:102-103) turned into probabilities with the
+    final maximum and denominator (:123-124), the sink folded into the
+    denominator (:117-120; "exp" mode adds e^z instead).  q [Hq, D];
+    k [L, Hkv, D]."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    Hq, D = q.shape
+    L, Hkv, _ = k.shape
+    G = Hq // Hkv
+    nb = -(-L // block)
+    n_blocks = nb if n_blocks is None else int(n_blocks)
+    out = np.zeros((Hq, n_blocks))
+    if L == 0:
+        return out
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
+    s = np.stack([k[:, h // G, :] @ q[h] for h in range(Hq)]) * scale      # [Hq, L]
+    m = s.max(axis=1, keepdims=True)
+    if sink is not None and sink_mode == "exp":
+        z = np.asarray(sink, dtype=np.float64)[:, None]
+        M = np.maximum(m, z)
+        e = np.exp(s - M)
+        den = e.sum(axis=1, keepdims=True) + np.exp(z - M)
+    else:
+        e = np.exp(s - m)
+        den = e.sum(axis=1, keepdims=True)
+        if sink is not None:
+            den = den + np.asarray(sink, dtype=np.float64)[:, None]
+    p = e / den
+    for j in range(min(nb, n_blocks)):
+        out[:, j] = p[:, j * block:(j + 1) * block].max(axis=1)
+    return out
+
+
+def block_scores_varlen(q, k, cu_seqlens, s_aux=None, sink_mode="exp", sm_scale=None, n_blocks=1):
+    """[B, Hq, n_blocks] block scores of varlen-packed sequences."""
+    cu = np.asarray(cu_seqlens, dtype=np.int64)
+    return np.stack([block_scores(q[b], k[cu[b]:cu[b + 1]], s_aux, sink_mode, sm_scale, n_blocks)
+                     for b in range(len(q))])
+
+
+def block_scores_paged(q, k_pool, block_table, seq_lens, s_aux=None, sink_mode="exp", sm_scale=None,
+                       n_blocks=1, k_scale=None):
+    """[B, Hq, n_blocks] block scores through the paged addressing."""
+    outs = []
+    for b in range(len(q)):
+        k = paged_rows(k_pool, block_table, b, int(seq_lens[b]))
+        if k_scale is not None:
+            k = dequantize_fp8(k, k_scale)
+        outs.append(block_scores(q[b], k, s_aux, sink_mode, sm_scale, n_blocks))
     return np.stack(outs)
 
 

@@ -281,9 +281,47 @@ def pin_ref_cache(ora):
         return "Out of KV pages" in str(e)
 
 
+def _torch_probs(q, k, sink=None):
+    """Softmax weights from torch.softmax (exp sink = extra logit, then dropped)."""
+    Hq, D = q.shape
+    L, Hkv, _ = k.shape
+    G = Hq // Hkv
+    K = torch.tensor(k).permute(1, 0, 2).repeat_interleave(G, 0)           # [Hq, L, D]
+    s = torch.einsum("hd,hld->hl", torch.tensor(q), K) / math.sqrt(D)
+    if sink is not None:
+        s = torch.cat([s, torch.tensor(sink, dtype=s.dtype)[:, None]], 1)
+        return torch.softmax(s, 1)[:, :L].numpy()
+    return torch.softmax(s, 1).numpy()
+
+
+def pin_block_scores(ora):
+    for L in (1, 127, 128, 129, 300, 1000):
+        q, k, _ = rand_case(8, 2, 32, L)
+        z = rng.standard_normal(8)
+        for sink in (None, z):
+            p = _torch_probs(q, k, sink)
+            want = np.zeros((8, 10))
+            for j in range(min(10, -(-L // 128))):                          # brute-force block maxima
+                for h in range(8):
+                    want[h, j] = max(p[h, t] for t in range(128 * j, min(128 * j + 128, L)))
+            if not np.allclose(ora.block_scores(q, k, sink, "exp", n_blocks=10), want, atol=1e-14, rtol=1e-12):
+                return False
+        # linear sink: every probability scales by l / (l + z), l = sum e^{s - max} (logsumexp)
+        zl = np.abs(z) + 0.5
+        s = torch.tensor(np.stack([k[:, h // 4, :] @ q[h] for h in range(8)]) / math.sqrt(32))
+        l = torch.exp(torch.logsumexp(s, 1) - s.max(1).values).numpy()
+        plain = ora.block_scores(q, k, None, n_blocks=10)
+        if not np.allclose(ora.block_scores(q, k, zl, "linear", n_blocks=10), plain * (l / (l + zl))[:, None],
+                           atol=1e-14, rtol=1e-12):
+            return False
+    if ora.block_scores(np.ones((2, 8)), np.ones((1, 1, 8)), n_blocks=3).tolist() != [[1, 0, 0], [1, 0, 0]]:
+        return False
+    return ora.block_scores(np.ones((2, 8)), np.zeros((0, 1, 8)), n_blocks=2).tolist() == [[0, 0], [0, 0]]
+
+
 PINS = [pin_sdpa, pin_exp_sink, pin_linear_sink, pin_golden_varlen, pin_golden_paged,
         pin_split_merge, pin_closed_forms, pin_layouts, pin_gather, pin_kv_encode, pin_paged_write,
-        pin_ref_cache]
+        pin_ref_cache, pin_block_scores]
 
 
 @pytest.mark.parametrize("pin", PINS, ids=lambda f: f.__name__)
@@ -434,6 +472,28 @@ class _FifoCache(O.RefPagedKVCache):
         super().append_kv(sid, layer, k, v)
 
 
+_block_scores_orig = O.block_scores
+
+
+def _block_scores_block64(q, k, sink=None, sink_mode="exp", sm_scale=None, n_blocks=None, block=128):
+    return _block_scores_orig(q, k, sink, sink_mode, sm_scale, n_blocks, block=64)
+
+
+def _block_scores_no_sink(q, k, sink=None, sink_mode="exp", sm_scale=None, n_blocks=None, block=128):
+    return _block_scores_orig(q, k, None, sink_mode, sm_scale, n_blocks, block)
+
+
+def _block_scores_sum(q, k, sink=None, sink_mode="exp", sm_scale=None, n_blocks=None, block=128):
+    # block sum instead of block max
+    full = _block_scores_orig(q, k, sink, sink_mode, sm_scale, None, 1)   # per-token probabilities
+    L = full.shape[1]
+    n = -(-L // block) if n_blocks is None else n_blocks
+    out = np.zeros((full.shape[0], n))
+    for j in range(min(n, -(-L // block))):
+        out[:, j] = full[:, j * block:(j + 1) * block].sum(1)
+    return out
+
+
 MUTANTS = {
     "head mapping h % Hkv": Mutant(attend=_attend_variant("headmap")),
     "sm_scale dropped": Mutant(attend=_attend_variant("noscale")),
@@ -447,6 +507,9 @@ MUTANTS = {
     "e4m3 tie at 464 encodes NaN": Mutant(e4m3_encode=_e4m3_encode_tie_to_nan),
     "quantiser without clamp": Mutant(encode_kv=_encode_kv_no_clamp),
     "free list FIFO": Mutant(RefPagedKVCache=_FifoCache),
+    "score block of 64": Mutant(block_scores=_block_scores_block64),
+    "scores ignore the sink": Mutant(block_scores=_block_scores_no_sink),
+    "scores pool by sum": Mutant(block_scores=_block_scores_sum),
 }
 
 
