@@ -13,6 +13,12 @@ GB/s; ``us_per_step`` and ``pct_of_peak`` (of 8 TB/s) are reported beside it.
 ``roofline`` is the split-KV partial kernel alone, timed with HIP events on
 the launch stream over the timed region.  ``cpu_baseline`` times the CPU
 oracle on a bounded sample of the same workload.
+
+Other workloads: ``--config C1..C5`` (decode configurations), ``--config
+W0..W2`` (the KV write path: a step is one store of a batch of new rows into
+scattered pages; ``roofline`` is the write kernel).  ``--graph`` replays each
+decode step from a captured HIP graph; ``--block-scores`` also computes the
+pooled 128-token block scores.
 """
 from __future__ import annotations
 
