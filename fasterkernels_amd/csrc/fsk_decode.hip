@@ -249,17 +249,26 @@ __device__ __forceinline__ HalfTile half_tile(const Params& p, int b, int start,
   return h;
 }
 
-// Chooses the split size from the actual sequence lengths and builds the unit
-// prefix table in LDS (pre[b] = first unit of sequence b, pre[B] = total).
-// The split is the larger of
-//   * total_tokens / target_units (enough units to fill the GPU), and
-//   * total_tokens / (u_max - B) (so every unit fits the workspace),
-// clamped to [chunk_min, chunk_max]; the host sizes u_max for chunk_max, so
-// the table always fits.  Workgroup 0 publishes the table for the reduce
-// kernel.  Every workgroup computes the same result from the same lengths.
+// Work plan.  The sequences' tokens are laid end to end, each sequence padded
+// to a multiple of kAlign (32 tokens, 128 with block scores), and the stream
+// is cut into equal chunks: work item (chunk j, head block) processes
+// stream positions [j*c, (j+1)*c) of one KV head.  A chunk that crosses
+// sequence boundaries is processed as one segment per sequence, and every
+// segment with valid tokens produces one fp32 partial, so all work items
+// carry the same number of tokens whatever the length distribution.
+//
+// The chunk c is the larger of
+//   * stream / target (target = target_units, doubled while the chunk would
+//     exceed chunk_max: enough equal chunks to fill the GPU evenly), and
+//   * stream / (u_max - B - 1) (so every partial fits the workspace: a batch
+//     has at most n_chunks + B partials),
+// rounded to kAlign and clamped to [chunk_min, chunk_max]; the host sizes
+// u_max for chunk_max.  In LDS: flat[b] = stream offset of sequence b
+// (flat[B] = stream length), pre[b] = first partial of sequence b (pre[B] =
+// total).  Workgroup 0 publishes pre for the reduce kernel.  Every workgroup
+// computes the same plan from the same lengths.  Returns the chunk count.
 template <int kLayout, bool kScores>
-__device__ int build_plan(const Params& p, int32_t* pre, int& chunk_out) {
-  // Split sizes are multiples of 32 tokens (one tile), of 128 with block scores.
+__device__ int build_plan(const Params& p, int32_t* pre, int32_t* flat, int& chunk_out) {
   constexpr int kAlign = kScores ? 128 : 32;
   const int lane = threadIdx.x;
   // Lengths of sequences lane, lane + 64, ...; the first block stays in a
@@ -269,31 +278,7 @@ __device__ int build_plan(const Params& p, int32_t* pre, int& chunk_out) {
     int start;
     seq_range<kLayout>(p, lane, start, len0);
   }
-  int64_t total = 0;
-  for (int b0 = 0; b0 < p.B; b0 += kWave) {
-    int len = len0;
-    if (b0 > 0) {
-      len = 0;
-      if (b0 + lane < p.B) {
-        int start;
-        seq_range<kLayout>(p, b0 + lane, start, len);
-      }
-    }
-    int sum = len;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, kWave);
-    total += sum;
-  }
-  int64_t want = (total + p.target_units - 1) / p.target_units;
-  if (p.u_max > p.B) want = std::max<int64_t>(want, (total + (p.u_max - p.B) - 1) / (p.u_max - p.B));
-  else want = p.chunk_max;
-  want = (want + kAlign - 1) / kAlign * kAlign;
-  const int chunk = uniform((int)std::min<int64_t>(std::max<int64_t>(want, p.chunk_min), p.chunk_max));
-  chunk_out = chunk;
-
-  int carry = 0;
-  for (int b0 = 0; b0 < p.B; b0 += kWave) {
-    const int b = b0 + lane;
+  auto length = [&](int b0, int b) {
     int len = len0;
     if (b0 > 0) {
       len = 0;
@@ -302,25 +287,67 @@ __device__ int build_plan(const Params& p, int32_t* pre, int& chunk_out) {
         seq_range<kLayout>(p, b, start, len);
       }
     }
-    const int n = (len + chunk - 1) / chunk;
-    int incl = n;
+    return b < p.B ? len : 0;
+  };
+  int64_t total = 0;
+  for (int b0 = 0; b0 < p.B; b0 += kWave) {
+    int sum = (length(b0, b0 + lane) + kAlign - 1) / kAlign * kAlign;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+    total += sum;
+  }
+  // Chunks per call: target_units, doubled while that would need chunks above
+  // chunk_max (a batch too long for target_units full-size chunks gets twice
+  // as many chunks rather than a count that leaves some CUs one item short).
+  int64_t target = p.target_units;
+  int64_t want = (total + target - 1) / target;
+  while (want > p.chunk_max && target < (1 << 24)) {
+    target *= 2;
+    want = (total + target - 1) / target;
+  }
+  if (p.u_max > p.B + 1) want = std::max<int64_t>(want, (total + (p.u_max - p.B - 1) - 1) / (p.u_max - p.B - 1));
+  else want = p.chunk_max;
+  want = (want + kAlign - 1) / kAlign * kAlign;
+  const int chunk = uniform((int)std::min<int64_t>(std::max<int64_t>(want, p.chunk_min), p.chunk_max));
+  chunk_out = chunk;
+
+  int carry_f = 0, carry_u = 0;
+  for (int b0 = 0; b0 < p.B; b0 += kWave) {
+    const int b = b0 + lane;
+    const int len = length(b0, b);
+    const int padded = (len + kAlign - 1) / kAlign * kAlign;
+    int incl_f = padded;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) {
-      const int y = __shfl_up(incl, off, kWave);
-      if (lane >= off) incl += y;
+      const int y = __shfl_up(incl_f, off, kWave);
+      if (lane >= off) incl_f += y;
     }
-    if (b < p.B) pre[b] = min(carry + incl - n, p.u_max);
+    const int fb = carry_f + incl_f - padded;
+    const int n = len > 0 ? (fb + len - 1) / chunk - fb / chunk + 1 : 0;
+    int incl_u = n;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int y = __shfl_up(incl_u, off, kWave);
+      if (lane >= off) incl_u += y;
+    }
+    if (b < p.B) {
+      flat[b] = fb;
+      pre[b] = min(carry_u + incl_u - n, p.u_max);  // the cap never binds with the host's u_max
+    }
     if constexpr (kScores)
       if (blockIdx.x == 0 && b < p.B) p.lens_out[b] = len;
-    carry += __shfl(incl, kWave - 1, kWave);
+    carry_f += __shfl(incl_f, kWave - 1, kWave);
+    carry_u += __shfl(incl_u, kWave - 1, kWave);
   }
-  const int total_units = min(carry, p.u_max);
-  if (lane == 0) pre[p.B] = total_units;
+  if (lane == 0) {
+    flat[p.B] = carry_f;
+    pre[p.B] = min(carry_u, p.u_max);
+  }
   __syncthreads();
   if (blockIdx.x == 0) {
     for (int b = lane; b <= p.B; b += kWave) p.plan[b] = pre[b];
   }
-  return total_units;
+  return (carry_f + chunk - 1) / chunk;
 }
 
 // Largest b with pre[b] <= u (u < pre[B]).
@@ -584,32 +611,41 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   static_assert(kKV != kBF16 || kQ == kBF16, "bf16 KV needs bf16 Q");
   static_assert(kKV != kF16 || kQ != kBF16, "f16 KV needs f16 Q");
 
-  extern __shared__ int32_t s_pre[];
+  extern __shared__ int32_t s_plan[];
+  int32_t* s_pre = s_plan;              // [B+1] first partial of each sequence
+  int32_t* s_flat = s_plan + p.B + 1;   // [B+1] stream offset of each sequence
   const int lane = threadIdx.x;
   const int g = lane >> 4;
   const int c = lane & 15;
 
   int chunk;
-  const int total_units = build_plan<kLayout, kScores>(p, s_pre, chunk);
+  const int n_chunks = build_plan<kLayout, kScores>(p, s_pre, s_flat, chunk);
   const int NH = p.Hkv * p.n_hb;
-  const int64_t W = (int64_t)total_units * NH;
+  const int64_t W = (int64_t)n_chunks * NH;
   const float k_scale = kKvFp8 ? p.k_scale[0] : 1.0f;
   const float v_scale = kKvFp8 ? p.v_scale[0] : 1.0f;
   const float sscale = p.score_scale * k_scale;
 
   for (int64_t w = blockIdx.x; w < W; w += gridDim.x) {
-    const int u = (int)(w / NH);
-    const int hh = (int)(w - (int64_t)u * NH);
+    const int jc = (int)(w / NH);
+    const int hh = (int)(w - (int64_t)jc * NH);
+    const int kvh = hh / p.n_hb;
+    const int hb = hh - kvh * p.n_hb;
+    const int lo = jc * chunk, hi = lo + chunk;  // stream range of this chunk
+    for (int b = uniform(find_seq(s_flat, p.B, lo)); b < p.B; ++b) {
+    const int fb = uniform(s_flat[b]);
+    if (fb >= hi) break;
     Unit un;
-    un.kvh = hh / p.n_hb;
-    const int hb = hh - un.kvh * p.n_hb;
-    un.b = uniform(find_seq(s_pre, p.B, u));
-    const int cidx = u - uniform(s_pre[un.b]);
+    un.b = b;
+    un.kvh = kvh;
     seq_range<kLayout>(p, un.b, un.start, un.len);
     un.start = uniform(un.start);
     un.len = uniform(un.len);
-    un.t_begin = cidx * chunk;
-    un.t_end = min(un.t_begin + chunk, un.len);
+    un.t_begin = max(lo - fb, 0);
+    un.t_end = min(hi - fb, un.len);
+    if (un.t_end <= un.t_begin) continue;  // only padding of sequence b in this chunk
+    const int u = uniform(s_pre[b]) + (jc - fb / chunk);  // this segment's partial
+    if (u >= p.u_max) continue;                          // (the host sizes u_max so this never holds)
     un.p_first = 0;
     un.win0 = un.win1 = 0;
     if constexpr (kLayout == kPaged) {
@@ -704,6 +740,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
         }
       if (g == 0) *(f32x2*)(p.part_ml + 2 * idx) = f32x2{st.m_run, l_tot};
     }
+    }  // segments of the chunk
   }
 }
 
@@ -1160,11 +1197,18 @@ inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 constexpr int kChunkMin = 128;   // smallest automatic split (tokens)
 constexpr int kChunkMax = 2048;  // largest split: 128 pages of 16 tokens per paged unit
 
-// Units a call can produce with split size `chunk` (host-side bound).
+// Longest padded token stream a call can have (each sequence is padded to a
+// multiple of at most 128 tokens on the device).
+int64_t stream_bound(int layout, int B, int64_t kv_extent, int page_size) {
+  if (layout == FSK_LAYOUT_VARLEN) return kv_extent + 128 * (int64_t)B;
+  if (layout == FSK_LAYOUT_PAGED) return (int64_t)B * (kv_extent * page_size + 128);
+  return (int64_t)B * (kv_extent + 128);
+}
+
+// Partials a call can produce with split size `chunk` (host-side bound): the
+// stream's chunks plus one more per sequence boundary.
 int64_t unit_bound(int layout, int B, int64_t kv_extent, int page_size, int chunk) {
-  if (layout == FSK_LAYOUT_VARLEN) return cdiv(kv_extent, chunk) + B;
-  if (layout == FSK_LAYOUT_PAGED) return (int64_t)B * cdiv(kv_extent * page_size, chunk);
-  return (int64_t)B * cdiv(kv_extent, chunk);
+  return cdiv(stream_bound(layout, B, kv_extent, page_size), chunk) + B + 1;
 }
 
 // Split policy of one call: a fixed split when the caller (or the
@@ -1273,6 +1317,8 @@ int validate(const Common& c) {
     if ((int64_t)c.max_blocks * c.page_size >= ((int64_t)1 << 31)) return fail(FSK_ERR_UNSUPPORTED, "block table too wide");
   }
   if (c.B > 16384) return fail(FSK_ERR_UNSUPPORTED, "batch above 16384");
+  if (stream_bound(c.layout, c.B, c.kv_extent, c.page_size > 0 ? c.page_size : 16) >= ((int64_t)1 << 31) - 4096)
+    return fail(FSK_ERR_UNSUPPORTED, "total token extent of the batch above 2^31");
   if (c.scores) {
     if (c.layout == FSK_LAYOUT_DENSE) return fail(FSK_ERR_UNSUPPORTED, "block scores on the varlen and paged layouts only");
     if (c.nblk <= 0 || c.nblk > (1 << 24)) return fail(FSK_ERR_INVALID, "score_blocks must be in [1, 2^24]");
@@ -1284,7 +1330,7 @@ int validate(const Common& c) {
 
 template <int D, int kQ, int kKV, int kLayout, bool kScores>
 void launch_partial(const Params& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((partial_kernel<D, kQ, kKV, kLayout, kScores>), dim3(grid), dim3(64), 4 * (p.B + 1), s, p);
+  hipLaunchKernelGGL((partial_kernel<D, kQ, kKV, kLayout, kScores>), dim3(grid), dim3(64), 8 * (p.B + 1), s, p);
 }
 
 template <int D, int kLayout, bool kScores>
