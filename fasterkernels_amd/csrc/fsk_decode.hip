@@ -396,12 +396,63 @@ template <int D, int kKV>
 struct TileRegs {
   static constexpr bool kFp8 = (kKV == kE4M3);
   static constexpr int kSteps = D / 32;
-  static constexpr int kKLoads = kFp8 ? kSteps / 2 : kSteps;  // 16-byte K loads per half
   static constexpr int kVBytes = (D / 16) * (kFp8 ? 1 : 2);   // V bytes per row per lane
-  u32x4 k[2][kKLoads];
+  static constexpr int kVLoads = kVBytes > 16 ? kVBytes / 16 : 1;
+  // K rows go through LDS (see issue_tile): 16 rows per half tile.
+  static constexpr int kRowBytes = D * (kFp8 ? 1 : 2);
+  static constexpr int kChunks = kRowBytes / 16;               // 16-byte chunks per K row
+  static constexpr int kHalfBytes = 16 * kRowBytes;
+  static constexpr int kDma = kHalfBytes / 1024;               // 16-byte-per-lane DMA loads per half
+  static constexpr int kLoads = 2 * kDma + 8 * kVLoads;        // vector memory instructions per tile
   Chunk<kVBytes> v[8];
   int nrow[2];  // valid rows of each 16-token half (wave-uniform)
 };
+
+// LDS pointers (address space 3): the K stage is addressed through these so
+// that no generic-to-LDS cast is needed.
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
+
+// 16-byte-per-lane DMA load into LDS: lane L's 16 bytes from byte voffset of
+// the buffer go to LDS offset lds_off + 16 L.  (Kept out of the templates:
+// the host pass of hipcc rejects this builtin inside a template.)
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds_off, int voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_u8*)(uintptr_t)lds_off, 16, voffset, 0, 0, kKvAux);
+}
+
+// K rows are staged in LDS with the 16-byte chunks of row R stored in the
+// order m ^ swz(R), so that the MFMA-operand reads (16 rows, one chunk each)
+// hit 16 different 16-byte bank groups.
+template <int kChunks>
+__device__ __forceinline__ int k_swizzle(int row) {
+  constexpr int kRowsPerCycle = kChunks >= 16 ? 1 : 16 / kChunks;
+  constexpr int kMask = (kChunks >= 16 ? 16 : kChunks) - 1;
+  return (row / kRowsPerCycle) & kMask;
+}
+
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector memory
+// operations are outstanding and leaves the other counters alone.
+constexpr int vm_wait_imm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | (((n >> 4) & 3) << 14); }
+
+// Waits for the K stage of a tile whose later tiles (``later`` of them, each
+// kLoads instructions) may still be in flight.  The LDS DMA writes are not
+// visible to the compiler's memory model, hence the explicit wait and the
+// compiler barrier that keeps the LDS reads after it.
+template <int kLoads, int kDepth>
+__device__ __forceinline__ void wait_k_stage(int later) {
+  static_assert(kLoads * (kDepth - 1) < 64, "vmcnt holds at most 63");
+  if constexpr (kDepth >= 3) {
+    if (later >= 2) __builtin_amdgcn_s_waitcnt(vm_wait_imm(2 * kLoads));
+    else if (later == 1) __builtin_amdgcn_s_waitcnt(vm_wait_imm(kLoads));
+    else __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
+  } else if constexpr (kDepth == 2) {
+    if (later >= 1) __builtin_amdgcn_s_waitcnt(vm_wait_imm(kLoads));
+    else __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
+  } else {
+    __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
+  }
+  asm volatile("" ::: "memory");
+}
 
 struct Unit {
   int b, kvh, start, len, t_begin, t_end;
@@ -432,11 +483,15 @@ __device__ __forceinline__ HalfTile unit_half(const Params& p, const Unit& un, i
 }
 
 template <int D, int kKV, int kLayout>
-__device__ __forceinline__ void issue_tile(TileRegs<D, kKV>& T, const Params& p, const Unit& un, int t,
-                                           int g, int c) {
+__device__ __forceinline__ void issue_tile(TileRegs<D, kKV>& T, uint32_t kstage_off, const Params& p,
+                                           const Unit& un, int t, int g, int c) {
   using TR = TileRegs<D, kKV>;
   constexpr int kElem = TR::kFp8 ? 1 : 2;
+  constexpr int kRowsPerDma = 64 / TR::kChunks;
   const int kst = (int)p.k_st, vst = (int)p.v_st;
+  const int lane = threadIdx.x;
+  // The stage is about to be overwritten: keep earlier LDS reads of it before this point.
+  asm volatile("" ::: "memory");
 #pragma unroll
   for (int h2 = 0; h2 < 2; ++h2) {
     const HalfTile ht = unit_half<kLayout>(p, un, t + 16 * h2);
@@ -445,15 +500,27 @@ __device__ __forceinline__ void issue_tile(TileRegs<D, kKV>& T, const Params& p,
     const int vbytes = ht.rows > 0 ? (ht.rows - 1) * vst + D * kElem : 0;
     const auto rk = make_rsrc(ht.k, kbytes);
     const auto rv = make_rsrc(ht.v, vbytes);
+    // K: coalesced 16-byte DMA loads straight into LDS (lane L of load r
+    // fetches row R = r * kRowsPerDma + L / kChunks, chunk (L % kChunks) ^
+    // swz(R); rows past the valid ones read as zero).
 #pragma unroll
-    for (int j = 0; j < TR::kKLoads; ++j) {
-      const Chunk<16> x = buf_load<16, kKvAux>(rk, c * kst + 16 * (4 * j + g));
-      T.k[h2][j] = u32x4{x.w[0], x.w[1], x.w[2], x.w[3]};
+    for (int r = 0; r < TR::kDma; ++r) {
+      const int R = r * kRowsPerDma + lane / TR::kChunks;
+      const int m = lane % TR::kChunks;
+      lds_dma16(rk, kstage_off + h2 * TR::kHalfBytes + r * 1024, R * kst + 16 * (m ^ k_swizzle<TR::kChunks>(R)));
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       T.v[4 * h2 + r] = buf_load<TR::kVBytes, kKvAux>(rv, (4 * g + r) * vst + c * TR::kVBytes);
   }
+}
+
+// 16-byte chunk `chunk` of K row c of half h2 from the LDS stage.
+template <int D, int kKV>
+__device__ __forceinline__ u32x4 k_chunk(uint32_t kstage_off, int h2, int c, int chunk) {
+  using TR = TileRegs<D, kKV>;
+  const uint32_t off = kstage_off + h2 * TR::kHalfBytes + 16 * (c * TR::kChunks + (chunk ^ k_swizzle<TR::kChunks>(c)));
+  return *(lds_u32x4*)(uintptr_t)off;
 }
 
 template <int D, int kQ, int kKV>
@@ -469,8 +536,9 @@ struct Softmax {
 // Returns the tile's maximum score of head column c (log2 domain, -inf when
 // the tile has no valid row).
 template <int D, int kQ, int kKV>
-__device__ __forceinline__ float compute_tile(const TileRegs<D, kKV>& T, Softmax<D, kQ, kKV>& st,
-                                              const u32x4 (&qop)[D / 32], float sscale, int g) {
+__device__ __forceinline__ float compute_tile(const TileRegs<D, kKV>& T, uint32_t kstage,
+                                              Softmax<D, kQ, kKV>& st, const u32x4 (&qop)[D / 32], float sscale,
+                                              int g, int c) {
   using TR = TileRegs<D, kKV>;
   using SM = Softmax<D, kQ, kKV>;
   constexpr int kSteps = SM::kSteps;
@@ -485,12 +553,13 @@ __device__ __forceinline__ float compute_tile(const TileRegs<D, kKV>& T, Softmax
     for (int i = 0; i < kSteps; ++i) {
       u32x4 kop;
       if constexpr (TR::kFp8) {
-        const u32x4 raw = T.k[h2][i >> 1];
+        // e4m3: chunk 4 (i / 2) + g holds k-steps i and i + 1
+        const u32x4 raw = k_chunk<D, kKV>(kstage, h2, c, 4 * (i >> 1) + g);
         const u32x2 a = e4m3x4_to<SM::kQkBf16>(raw[2 * (i & 1)]);
         const u32x2 bb = e4m3x4_to<SM::kQkBf16>(raw[2 * (i & 1) + 1]);
         kop = u32x4{a[0], a[1], bb[0], bb[1]};
       } else {
-        kop = T.k[h2][i];
+        kop = k_chunk<D, kKV>(kstage, h2, c, 4 * i + g);
       }
       s[h2] = mfma16x16x32<SM::kQkBf16>(kop, qop[i], s[h2]);
     }
@@ -611,6 +680,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   static_assert(kKV != kBF16 || kQ == kBF16, "bf16 KV needs bf16 Q");
   static_assert(kKV != kF16 || kQ != kBF16, "f16 KV needs f16 Q");
 
+  __shared__ __attribute__((aligned(16))) uint8_t s_kstage_mem[kDepth * 2 * TR::kHalfBytes];
+  // LDS offset of the stage = low 32 bits of its generic address
+  const uint32_t s_kstage = (uint32_t)(uintptr_t)s_kstage_mem;
   extern __shared__ int32_t s_plan[];
   int32_t* s_pre = s_plan;              // [B+1] first partial of each sequence
   int32_t* s_flat = s_plan + p.B + 1;   // [B+1] stream offset of each sequence
@@ -695,21 +767,29 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     BlockMax bm;
 
     if constexpr (kDepth > 1) {
-      // Tile slot s holds tile n with n % kDepth == s; while tile n is
-      // computed, tiles n+1 .. n+kDepth-1 are in flight.
+      // Tile slot s holds tile n with n % kDepth == s (its K stage is slot s
+      // of s_kstage); while tile n is computed, tiles n+1 .. n+kDepth-1 are
+      // in flight.
+      // Tiles past the unit's end are issued too: their buffer ranges are
+      // empty, so the loads read zeros without memory traffic, and every
+      // tile is computed with exactly kDepth - 1 later tiles in flight (a
+      // conditional issue would make the compiler wait for all loads).
       TR tiles[kDepth];
       int t = un.t_begin;
 #pragma unroll
       for (int s = 0; s < kDepth - 1; ++s)
-        if (t + 32 * s < un.t_end) issue_tile<D, kKV, kLayout>(tiles[s], p, un, t + 32 * s, g, c);
+        issue_tile<D, kKV, kLayout>(tiles[s], s_kstage + s * 2 * TR::kHalfBytes, p, un, t + 32 * s, g, c);
       bool done = false;
       while (!done) {
 #pragma unroll
         for (int s = 0; s < kDepth; ++s) {
           if (!done) {
             const int tn = t + 32 * (kDepth - 1);
-            if (tn < un.t_end) issue_tile<D, kKV, kLayout>(tiles[(s + kDepth - 1) % kDepth], p, un, tn, g, c);
-            const float mt = compute_tile<D, kQ, kKV>(tiles[s], st, qop, sscale, g);
+            const int sn = (s + kDepth - 1) % kDepth;
+            issue_tile<D, kKV, kLayout>(tiles[sn], s_kstage + sn * 2 * TR::kHalfBytes, p, un, tn, g, c);
+            wait_k_stage<TR::kLoads, kDepth>(kDepth - 1);
+            const float mt = compute_tile<D, kQ, kKV>(tiles[s], s_kstage + s * 2 * TR::kHalfBytes, st, qop,
+                                                      sscale, g, c);
             if constexpr (kScores) bm.add(p, un, t, mt, head, head_ok, g);
             t += 32;
             done = t >= un.t_end;
@@ -719,8 +799,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     } else {
       TR ta;
       for (int t = un.t_begin; t < un.t_end; t += 32) {
-        issue_tile<D, kKV, kLayout>(ta, p, un, t, g, c);
-        const float mt = compute_tile<D, kQ, kKV>(ta, st, qop, sscale, g);
+        issue_tile<D, kKV, kLayout>(ta, s_kstage, p, un, t, g, c);
+        wait_k_stage<TR::kLoads, 1>(0);
+        const float mt = compute_tile<D, kQ, kKV>(ta, s_kstage, st, qop, sscale, g, c);
         if constexpr (kScores) bm.add(p, un, t, mt, head, head_ok, g);
       }
     }
