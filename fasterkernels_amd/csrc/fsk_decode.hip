@@ -1361,7 +1361,10 @@ int validate(const Common& c) {
   if (c.B < 0 || c.Hq <= 0 || c.Hkv <= 0) return fail(FSK_ERR_INVALID, "batch/heads must be positive");
   if (c.Hq % c.Hkv != 0) return fail(FSK_ERR_INVALID, "num_q_heads must be a multiple of num_kv_heads");
   if (c.D != 64 && c.D != 128 && c.D != 256) return fail(FSK_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256");
-  if (!c.q || !c.k || !c.v || !c.lens || !c.out) return fail(FSK_ERR_INVALID, "null tensor pointer");
+  // An empty varlen/dense KV (extent 0: every sequence empty) reads no row, so
+  // its k/v may be null, as an empty tensor's data pointer is.
+  const bool kv_empty = c.layout != FSK_LAYOUT_PAGED && c.kv_extent == 0;
+  if (!c.q || !c.lens || !c.out || (!kv_empty && (!c.k || !c.v))) return fail(FSK_ERR_INVALID, "null tensor pointer");
   if (c.sink_mode != FSK_SINK_EXP && c.sink_mode != FSK_SINK_LINEAR) return fail(FSK_ERR_INVALID, "bad sink_mode");
   if (c.o_dt != FSK_F16 && c.o_dt != FSK_BF16 && c.o_dt != FSK_F32) return fail(FSK_ERR_UNSUPPORTED, "out dtype must be f16, bf16 or f32");
   if (c.kv_dt == FSK_E4M3) {

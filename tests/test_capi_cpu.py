@@ -116,6 +116,10 @@ def test_varlen_and_dense_validation(lib):
     bad = list(ok)
     bad[9] = None  # cu_seqlens
     assert lib.fsk_decode_varlen(*bad) == nat.FSK_ERR_INVALID
+    bad = list(ok)
+    bad[3] = None  # k, with 1000 rows
+    assert lib.fsk_decode_varlen(*bad) == nat.FSK_ERR_INVALID
+    assert b"null" in lib.fsk_last_error()
     dense = [FAKE, 32 * 128, 128, FAKE, 8 * 512 * 128, 512 * 128, 128, FAKE, 8 * 512 * 128, 512 * 128, 128,
              512, FAKE, None, None, 0, None, None, None, FAKE, 32 * 128, 128, 4, 32, 8, 128,
              nat.FSK_E4M3, nat.FSK_E4M3, nat.FSK_F16, 0.088, FAKE, 1 << 30, 0, None]

@@ -331,3 +331,12 @@ def test_zero_length_with_very_negative_sink():
     wl = W.make("C1", overrides=dict(B=3, lens=("list", [0, 5, 0]), sinks=True), seed=35)
     wl.s_aux = torch.full_like(wl.s_aux, -200.0)
     run_and_check(wl, what="empty + sink -200")
+
+
+@pytest.mark.parametrize("sinks", [False, True])
+def test_all_empty_varlen_batch(sinks):
+    """Every sequence empty and K/V with zero rows (null data pointers): the
+    oracle's output for empty sequences (NaN without sinks, 0 with them)."""
+    wl = W.make("C1", overrides=dict(B=4, lens=("list", [0, 0, 0, 0]), sinks=sinks), seed=36)
+    assert wl.k.shape[0] == 0
+    run_and_check(wl, what=f"all empty, sinks={sinks}")
