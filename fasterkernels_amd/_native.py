@@ -109,13 +109,31 @@ def check(status: int) -> None:
 
 def set_option(name: str, value: int) -> None:
     check(load().fsk_set_option(name.encode(), int(value)))
+    _WS_CACHE.clear()  # workspace sizes follow the split options
+
+
+# (device, layout, batch, hq, hkv, d, kv_extent, page_size, chunk_tokens) -> bytes
+_WS_CACHE: dict = {}
 
 
 def workspace_bytes(layout: int, batch: int, hq: int, hkv: int, d: int, kv_extent: int,
-                    page_size: int = 16, chunk_tokens: int = 0) -> int:
-    n = load().fsk_workspace_bytes(layout, batch, hq, hkv, d, kv_extent, page_size, chunk_tokens)
+                    page_size: int = 16, chunk_tokens: int = 0, device_index: int | None = None) -> int:
+    """fsk_workspace_bytes for the current device, or for ``device_index``
+    (then cached: the size depends only on the arguments, the device's CU
+    count and the library options)."""
+    key = (device_index, layout, batch, hq, hkv, d, kv_extent, page_size, chunk_tokens)
+    if device_index is not None:
+        n = _WS_CACHE.get(key)
+        if n is not None:
+            return n
+        n = launch(device_index, load().fsk_workspace_bytes, layout, batch, hq, hkv, d, kv_extent, page_size,
+                   chunk_tokens)
+    else:
+        n = load().fsk_workspace_bytes(layout, batch, hq, hkv, d, kv_extent, page_size, chunk_tokens)
     if n < 0:
         check(int(n))
+    if device_index is not None:
+        _WS_CACHE[key] = int(n)
     return int(n)
 
 
@@ -130,8 +148,24 @@ def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-def stream_handle(device: torch.device) -> int:
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def stream_handle(device: torch.device | int) -> int:
+    """Handle of torch's current stream on ``device``."""
+    index = device if isinstance(device, int) else device.index
+    if _raw_stream is not None and index is not None:
+        return _raw_stream(index)
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def launch(device_index: int, fn, *args):
+    """fn(*args) with ``device_index`` as the current HIP device (switched only
+    when it is not already current)."""
+    if torch._C._cuda_getDevice() == device_index:
+        return fn(*args)
+    with torch.cuda.device(device_index):
+        return fn(*args)
 
 
 def enable_kernel_timing(every_n: int = 1) -> None:

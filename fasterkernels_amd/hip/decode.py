@@ -65,12 +65,14 @@ def _on_gpu(t: torch.Tensor, name: str, device: torch.device | None = None) -> N
         raise TypeError(f"{name} must be a torch.Tensor")
     if not t.is_cuda:
         raise RuntimeError(f"{name} must be on a GPU (HIP) device")
-    if device is not None and t.device != device:
+    if device is not None and t.get_device() != device.index:
         raise RuntimeError(f"{name} is on {t.device}, expected {device}")
 
 
 def _inner_contig(t: torch.Tensor) -> torch.Tensor:
     """Innermost dim contiguous with 16-byte aligned rows, else a packed copy."""
+    if t.is_contiguous() and t.data_ptr() % 16 == 0 and (t.shape[-1] * t.element_size()) % 16 == 0:
+        return t
     es = t.element_size()
     ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(
         (s * es) % 16 == 0 for s in t.stride()[:-1])
@@ -86,6 +88,8 @@ def _dtype_code(dt: torch.dtype, name: str) -> int:
 
 def _int32(t: torch.Tensor, name: str, device: torch.device) -> torch.Tensor:
     _on_gpu(t, name, device)
+    if t.dtype is torch.int32 and t.is_contiguous():
+        return t
     if t.dtype != torch.int32:
         t = t.to(torch.int32)
     return t.contiguous()
@@ -100,8 +104,9 @@ def _scale_ptr(s, device, name):
     _on_gpu(s, name, device)
     if s.numel() != 1:
         raise ValueError(f"{name} must hold a single per-tensor scale")
-    s = s.reshape(()).to(torch.float32).contiguous()
-    return s, s.data_ptr()
+    if s.dtype is not torch.float32:
+        s = s.to(torch.float32)
+    return s, s.data_ptr()  # one element: its address whatever the shape and strides
 
 
 def _sinks(s_aux, hq, device):
@@ -110,6 +115,8 @@ def _sinks(s_aux, hq, device):
     _on_gpu(s_aux, "s_aux", device)
     if s_aux.numel() != hq:
         raise ValueError(f"s_aux must have num_q_heads={hq} entries, got {tuple(s_aux.shape)}")
+    if s_aux.dtype is torch.float32 and s_aux.is_contiguous():
+        return s_aux
     return s_aux.reshape(hq).to(torch.float32).contiguous()
 
 
@@ -177,7 +184,7 @@ def flash_decode_gqa_varlen(q, k_varlen, v_varlen, cu_seqlens_k, s_aux=None, *,
     odt = out_dtype or q.dtype
     out = torch.empty((B, Hq, D), dtype=odt, device=dev)
     scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
-    nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_VARLEN, B, Hq, Hkv, D, T, 16, chunk_tokens)
+    nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_VARLEN, B, Hq, Hkv, D, T, 16, chunk_tokens, dev.index)
     scores, nblk = _scores_out(return_block_scores, score_blocks, T, B, Hq, odt, dev)
     if scores is not None:
         nbytes += nat.score_workspace_bytes(B, Hq, nblk)
@@ -190,11 +197,11 @@ def flash_decode_gqa_varlen(q, k_varlen, v_varlen, cu_seqlens_k, s_aux=None, *,
             out.data_ptr(), out.stride(0), out.stride(1),
             B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_varlen"),
             _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens)
-    with torch.cuda.device(dev):
-        if scores is None:
-            st = lib.fsk_decode_varlen(*args, nat.stream_handle(dev))
-        else:
-            st = lib.fsk_decode_varlen_scores(*args, scores.data_ptr(), nblk, nat.stream_handle(dev))
+    if scores is None:
+        st = nat.launch(dev.index, lib.fsk_decode_varlen, *args, nat.stream_handle(dev))
+    else:
+        st = nat.launch(dev.index, lib.fsk_decode_varlen_scores, *args, scores.data_ptr(), nblk,
+                        nat.stream_handle(dev))
     nat.check(st)
     return out if scores is None else (out, scores)
 
@@ -240,19 +247,19 @@ def _dense(q, k_cache, v_cache, cache_lens, start_k_offsets, num_splits, *, q_sc
     scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
     if not chunk_tokens and num_splits and num_splits > 1:
         chunk_tokens = max(32, -(-math.ceil(S / num_splits) // 32) * 32)
-    nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_DENSE, B, Hq, Hkv, D, S, 16, chunk_tokens)
+    nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_DENSE, B, Hq, Hkv, D, S, 16, chunk_tokens, dev.index)
     ws = _workspace(nbytes, dev)
     lib = nat.load()
-    with torch.cuda.device(dev):
-        st = lib.fsk_decode_dense(
-            q.data_ptr(), q.stride(0), q.stride(1),
-            k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
-            v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), S,
-            lens.data_ptr(), nat.ptr(starts), nat.ptr(sinks), _sink_mode(sink_mode), qsp, ksp, vsp,
-            out.data_ptr(), out.stride(0), out.stride(1),
-            B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_cache"),
-            _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens,
-            nat.stream_handle(dev))
+    st = nat.launch(
+        dev.index, lib.fsk_decode_dense,
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), S,
+        lens.data_ptr(), nat.ptr(starts), nat.ptr(sinks), _sink_mode(sink_mode), qsp, ksp, vsp,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_cache"),
+        _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens,
+        nat.stream_handle(dev))
     nat.check(st)
     return out
 
@@ -338,7 +345,7 @@ def paged_flash_decode(q, k_pool, v_pool, block_table, seq_lens, page_size, *, s
     out = torch.empty((B, Hq, D), dtype=odt, device=dev)
     scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
     max_blocks = bt.shape[1]
-    nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_PAGED, B, Hq, Hkv, D, max_blocks, PS, chunk_tokens)
+    nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_PAGED, B, Hq, Hkv, D, max_blocks, PS, chunk_tokens, dev.index)
     scores, nblk = _scores_out(return_block_scores, score_blocks, max_blocks * PS, B, Hq, odt, dev)
     if scores is not None:
         nbytes += nat.score_workspace_bytes(B, Hq, nblk)
@@ -352,11 +359,11 @@ def paged_flash_decode(q, k_pool, v_pool, block_table, seq_lens, page_size, *, s
             out.data_ptr(), out.stride(0), out.stride(1),
             B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_pool"),
             _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens)
-    with torch.cuda.device(dev):
-        if scores is None:
-            st = lib.fsk_decode_paged(*args, nat.stream_handle(dev))
-        else:
-            st = lib.fsk_decode_paged_scores(*args, scores.data_ptr(), nblk, nat.stream_handle(dev))
+    if scores is None:
+        st = nat.launch(dev.index, lib.fsk_decode_paged, *args, nat.stream_handle(dev))
+    else:
+        st = nat.launch(dev.index, lib.fsk_decode_paged_scores, *args, scores.data_ptr(), nblk,
+                        nat.stream_handle(dev))
     nat.check(st)
     return out if scores is None else (out, scores)
 
@@ -376,11 +383,9 @@ def paged_gather(pool, block_table, seq_lens):
     B, MB = bt.shape
     out = torch.empty((B, Hkv, MB * PS, D), dtype=pool.dtype, device=dev)
     lib = nat.load()
-    with torch.cuda.device(dev):
-        st = lib.fsk_paged_gather(pool.data_ptr(), pool.stride(0), pool.stride(1), pool.stride(2),
-                                  bt.data_ptr(), bt.stride(0), MB, lens.data_ptr(), P, PS, B, Hkv,
-                                  D, _dtype_code(pool.dtype, "pool"), out.data_ptr(),
-                                  nat.stream_handle(dev))
+    st = nat.launch(dev.index, lib.fsk_paged_gather, pool.data_ptr(), pool.stride(0), pool.stride(1),
+                    pool.stride(2), bt.data_ptr(), bt.stride(0), MB, lens.data_ptr(), P, PS, B, Hkv, D,
+                    _dtype_code(pool.dtype, "pool"), out.data_ptr(), nat.stream_handle(dev))
     nat.check(st)
     return out
 
@@ -391,8 +396,7 @@ def fp8_decode_table(device="cuda"):
     dev = torch.device(device)
     out = torch.empty(512, dtype=torch.int16, device=dev)
     lib = nat.load()
-    with torch.cuda.device(dev):
-        st = lib.fsk_fp8_decode_table(out.data_ptr(), nat.stream_handle(dev))
+    st = nat.launch(dev.index, lib.fsk_fp8_decode_table, out.data_ptr(), nat.stream_handle(dev))
     nat.check(st)
     bits = out.cpu()
     return torch.stack([bits[:256].view(torch.float16).to(torch.float32),

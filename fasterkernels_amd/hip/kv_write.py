@@ -65,7 +65,7 @@ def paged_kv_write(k: torch.Tensor, v: torch.Tensor, k_pool: torch.Tensor, v_poo
         if t.stride(-1) != 1:
             raise ValueError(f"{name} must have a contiguous head_dim")
     dev = k_pool.device
-    if v_pool.device != dev or v_pool.shape != k_pool.shape or v_pool.dtype != k_pool.dtype:
+    if v_pool.get_device() != dev.index or v_pool.shape != k_pool.shape or v_pool.dtype != k_pool.dtype:
         raise ValueError("k_pool and v_pool must match in shape, dtype and device")
     P, Hkv, ps, D = k_pool.shape
     k = _rows(k, "k")
@@ -78,7 +78,8 @@ def paged_kv_write(k: torch.Tensor, v: torch.Tensor, k_pool: torch.Tensor, v_poo
     _on_gpu(slot_mapping, "slot_mapping", dev)
     if slot_mapping.dtype != torch.int64 or slot_mapping.numel() != n:
         raise ValueError(f"slot_mapping must be int64 with {n} entries")
-    slot_mapping = slot_mapping.reshape(n).contiguous()
+    if slot_mapping.dim() != 1 or not slot_mapping.is_contiguous():
+        slot_mapping = slot_mapping.reshape(n).contiguous()
     ks = _scale(k_scale, "k_scale", dev)
     vs = _scale(v_scale, "v_scale", dev)
     bt_ptr, bt_numel, upd_ptr, n_upd = None, 0, None, 0
@@ -95,12 +96,12 @@ def paged_kv_write(k: torch.Tensor, v: torch.Tensor, k_pool: torch.Tensor, v_poo
         bt_ptr, bt_numel = block_table.data_ptr(), block_table.numel()
         upd_ptr, n_upd = bt_updates.data_ptr(), bt_updates.shape[0]
     lib = nat.load()
-    with torch.cuda.device(dev):
-        st = lib.fsk_paged_write(
-            k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
-            slot_mapping.data_ptr(), n,
-            k_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
-            v_pool.data_ptr(), v_pool.stride(0), v_pool.stride(1), v_pool.stride(2),
-            P, ps, Hkv, D, nat.DTYPE_CODES[k.dtype], nat.DTYPE_CODES[k_pool.dtype],
-            nat.ptr(ks), nat.ptr(vs), bt_ptr, bt_numel, upd_ptr, n_upd, nat.stream_handle(dev))
+    st = nat.launch(
+        dev.index, lib.fsk_paged_write,
+        k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
+        slot_mapping.data_ptr(), n,
+        k_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
+        v_pool.data_ptr(), v_pool.stride(0), v_pool.stride(1), v_pool.stride(2),
+        P, ps, Hkv, D, nat.DTYPE_CODES[k.dtype], nat.DTYPE_CODES[k_pool.dtype],
+        nat.ptr(ks), nat.ptr(vs), bt_ptr, bt_numel, upd_ptr, n_upd, nat.stream_handle(dev))
     nat.check(st)
