@@ -720,12 +720,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     if (u >= p.u_max) continue;                          // (the host sizes u_max so this never holds)
     un.p_first = 0;
     un.win0 = un.win1 = 0;
+    int win_raw0 = 0, win_raw1 = 0;
     if constexpr (kLayout == kPaged) {
       un.p_first = un.t_begin / p.page_size;
       const int npg = (un.t_end - 1) / p.page_size - un.p_first + 1;  // <= 128 (chunk <= 2048)
       const int32_t* row = p.block_table + (int64_t)un.b * p.bt_sb + un.p_first;
-      if (lane < npg) un.win0 = clampi(row[lane], 0, p.num_pages - 1);
-      if (lane + 64 < npg) un.win1 = clampi(row[lane + 64], 0, p.num_pages - 1);
+      // Two range-checked loads (entries past npg read as 0) without
+      // branches, so they and the Q loads below share one memory round trip;
+      // the page ids are clamped to the pool once Q is in flight.
+      const auto rw = make_rsrc(row, 4 * npg);
+      win_raw0 = (int)buf_load<4>(rw, 4 * lane).w[0];
+      win_raw1 = (int)buf_load<4>(rw, 4 * (lane + 64)).w[0];
     }
 
     // ---- Q^T operand: head c of this head block, zero for padding heads.
@@ -738,25 +743,29 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
 #pragma unroll
       for (int i = 0; i < kSteps; ++i) {
         const int d0 = qk_dim0<kKvFp8>(i, g);
-        u32x4 x = {0, 0, 0, 0};
-        if (head_ok) {
-          if constexpr (kQ == kE4M3) {
-            // q = f16(f32(q8) * scale_q)  (triton_gqa_decode_hf_fp8.py:47-50)
-            const u32x2 raw = *(const u32x2*)(qrow + d0);
-            const float sq = p.q_scale[0];
+        // Every lane loads (padding heads read head 0's row, then zero it):
+        // unconditional loads keep the compiler's wait counts exact.
+        u32x4 x;
+        if constexpr (kQ == kE4M3) {
+          // q = f16(f32(q8) * scale_q)  (triton_gqa_decode_hf_fp8.py:47-50)
+          const u32x2 raw = *(const u32x2*)(qrow + d0);
+          const float sq = p.q_scale[0];
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-              const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(raw[e], false);
-              const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(raw[e], true);
-              x[2 * e] = pack_f16x2(lo[0] * sq, lo[1] * sq);
-              x[2 * e + 1] = pack_f16x2(hi[0] * sq, hi[1] * sq);
-            }
-          } else {
-            x = *(const u32x4*)(qrow + 2 * d0);
+          for (int e = 0; e < 2; ++e) {
+            const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(raw[e], false);
+            const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(raw[e], true);
+            x[2 * e] = pack_f16x2(lo[0] * sq, lo[1] * sq);
+            x[2 * e + 1] = pack_f16x2(hi[0] * sq, hi[1] * sq);
           }
+        } else {
+          x = *(const u32x4*)(qrow + 2 * d0);
         }
-        qop[i] = x;
+        qop[i] = head_ok ? x : u32x4{0, 0, 0, 0};
       }
+    }
+    if constexpr (kLayout == kPaged) {
+      un.win0 = clampi(win_raw0, 0, p.num_pages - 1);
+      un.win1 = clampi(win_raw1, 0, p.num_pages - 1);
     }
 
     SM st;
