@@ -4,8 +4,8 @@
 A step is one decode call over one batch (default: the headline workload M0,
 paged fp16 KV, B=4, Hq=32, Hkv=8, D=128, 32768 tokens per sequence, 16-token
 pages scattered by a seeded permutation).  Inputs are generated on the GPU and
-are resident in HBM before timing; several independent input sets are rotated
-so the working set exceeds the 256 MB Infinity Cache.
+are resident in HBM before timing; at least 4 independent input sets are
+rotated, with a footprint above 1.1 GB, beyond the 256 MB Infinity Cache.
 
 Prints one JSON line.  ``value`` is the achieved algorithmic HBM bandwidth of a
 whole step (valid K+V bytes + Q + output + block-table entries + lengths) in
@@ -39,7 +39,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="M0", help="workload name (decode: M0, C1..C5; KV write: W0..W2)")
-    ap.add_argument("--sets", type=int, default=0, help="input sets to rotate (0: enough for >1 GB)")
+    ap.add_argument("--sets", type=int, default=0, help="input sets to rotate (0: >= 4 and enough for > 1.1 GB)")
     ap.add_argument("--chunk", type=int, default=0, help="split size in tokens (0: library default)")
     ap.add_argument("--block-scores", action="store_true",
                     help="also compute the pooled 128-token block scores in each step")
@@ -53,6 +53,13 @@ def parse():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration under rocprof)")
     return ap.parse_args()
+
+
+def rotation_sets(bytes_per_set: int) -> int:
+    """Independent input sets rotated through the timed steps: at least 4, and
+    enough that their footprint exceeds 1.1 GB (4x the 256 MB Infinity Cache),
+    so no step reads another step's data out of cache."""
+    return max(4, min(128, -(-1_100_000_000 // max(1, bytes_per_set))))
 
 
 def copy_calibration(nbytes: int) -> None:
@@ -188,7 +195,7 @@ def bench_write(args):
     torch.cuda.set_device(dev)
     base = W.make_write(args.config, device=dev)
     alg_bytes = base.algorithmic_bytes()
-    n_sets = args.sets or max(1, min(8, -(-1_100_000_000 // alg_bytes)))
+    n_sets = args.sets or rotation_sets(alg_bytes)
     sets = [base] + [W.make_write(args.config, device=dev, data_seed=base.meta["seed"] + 1000 * i)
                      for i in range(1, n_sets)]
     for i in range(args.warmup):
@@ -272,7 +279,7 @@ def main():
     torch.cuda.set_device(dev)
     base = W.make(args.config, gen_device=dev, device=dev)
     kv_bytes = base.k.numel() * base.k.element_size() * 2
-    n_sets = args.sets or max(1, min(8, -(-1_100_000_000 // kv_bytes)))
+    n_sets = args.sets or rotation_sets(kv_bytes)
     # same lengths and page tables, independent K/V data
     sets = [base] + [W.make(args.config, gen_device=dev, device=dev, data_seed=base.meta["seed"] + 1000 * i)
                      for i in range(1, n_sets)]
