@@ -268,16 +268,17 @@ __device__ __forceinline__ HalfTile half_tile(const Params& p, int b, int start,
 // total).  Workgroup 0 publishes pre for the reduce kernel.  Every workgroup
 // computes the same plan from the same lengths.  Returns the chunk count.
 template <int kLayout, bool kScores>
-__device__ int build_plan(const Params& p, int32_t* pre, int32_t* flat, int& chunk_out) {
+__device__ int build_plan(const Params& p, int32_t* pre, int32_t* flat, int& chunk_out, int& start0_out,
+                          int& len0_out) {
   constexpr int kAlign = kScores ? 128 : 32;
   const int lane = threadIdx.x;
   // Lengths of sequences lane, lane + 64, ...; the first block stays in a
-  // register so that the common case (B <= 64) reads them once.
-  int len0 = 0;
-  if (lane < p.B) {
-    int start;
-    seq_range<kLayout>(p, lane, start, len0);
-  }
+  // register so that the common case (B <= 64) reads them once (and the
+  // work loop reads them from these registers, not from memory).
+  int len0 = 0, start0 = 0;
+  if (lane < p.B) seq_range<kLayout>(p, lane, start0, len0);
+  start0_out = start0;
+  len0_out = len0;
   auto length = [&](int b0, int b) {
     int len = len0;
     if (b0 > 0) {
@@ -690,8 +691,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   const int g = lane >> 4;
   const int c = lane & 15;
 
-  int chunk;
-  const int n_chunks = build_plan<kLayout, kScores>(p, s_pre, s_flat, chunk);
+  int chunk, lane_start, lane_len;  // start and length of sequence `lane` (B <= 64)
+  const int n_chunks = build_plan<kLayout, kScores>(p, s_pre, s_flat, chunk, lane_start, lane_len);
   const int NH = p.Hkv * p.n_hb;
   const int64_t W = (int64_t)n_chunks * NH;
   const float k_scale = kKvFp8 ? p.k_scale[0] : 1.0f;
@@ -710,9 +711,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     Unit un;
     un.b = b;
     un.kvh = kvh;
-    seq_range<kLayout>(p, un.b, un.start, un.len);
-    un.start = uniform(un.start);
-    un.len = uniform(un.len);
+    if (p.B <= kWave) {
+      un.start = __builtin_amdgcn_readlane(lane_start, un.b);
+      un.len = __builtin_amdgcn_readlane(lane_len, un.b);
+    } else {
+      seq_range<kLayout>(p, un.b, un.start, un.len);
+      un.start = uniform(un.start);
+      un.len = uniform(un.len);
+    }
     un.t_begin = max(lo - fb, 0);
     un.t_end = min(hi - fb, un.len);
     if (un.t_end <= un.t_begin) continue;  // only padding of sequence b in this chunk

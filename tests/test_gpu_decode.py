@@ -340,3 +340,34 @@ def test_all_empty_varlen_batch(sinks):
     wl = W.make("C1", overrides=dict(B=4, lens=("list", [0, 0, 0, 0]), sinks=sinks), seed=36)
     assert wl.k.shape[0] == 0
     run_and_check(wl, what=f"all empty, sinks={sinks}")
+
+
+# ---------------------------------------------------------------------------
+# batches above one wave (B > 64): the plan scans several blocks of lengths
+# and the work loop reads lengths from memory instead of registers
+# ---------------------------------------------------------------------------
+def _lens(B, hi, seed):
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(0, hi, (B,), generator=g).tolist()
+    lens[3] = 0
+    lens[-1] = hi  # the longest sequence last
+    return lens
+
+
+@pytest.mark.parametrize("layout", ["varlen", "paged"])
+def test_batches_above_one_wave(layout):
+    name = "C1" if layout == "varlen" else "C3"
+    lens = _lens(150, 400, 51)
+    wl = W.make(name, overrides=dict(B=150, lens=("list", lens), sinks=True), seed=52)
+    run_and_check(wl, what=f"{layout} B=150")
+    run_and_check(wl, chunk_tokens=64, what=f"{layout} B=150 chunk 64")
+
+
+def test_dense_batch_above_one_wave():
+    B = 70
+    lens = _lens(B, 300, 53)
+    starts = [min(L, (7 * i) % 50) for i, L in enumerate(lens)]
+    q, k, v, lt, st = _dense_inputs(B, 300, lens, starts, torch.bfloat16, 8)
+    out = dec.flash_decode_gqa_hf_dense_optimized(q.to(DEV), k.to(DEV), v.to(DEV), lt.to(DEV), st.to(DEV))
+    ref = O.decode_dense(f64(q), f64(k), f64(v), lt.numpy(), st.numpy())
+    assert_close(out, ref, 2e-3, 2e-3, "dense B=70")
