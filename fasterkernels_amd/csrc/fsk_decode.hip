@@ -77,6 +77,20 @@ __device__ __forceinline__ float group4_sum(float x) {
   return u2f(b[0]) + u2f(b[1]);
 }
 
+// Inclusive prefix sum over the 64 lanes with DPP: row_shr 1, 2, 4, 8 scan
+// each row of 16 lanes, then row_bcast:15 adds row 0's total to row 1 and
+// row 2's to row 3, and row_bcast:31 adds the total of rows 0-1 to rows 2-3
+// (lanes a DPP step does not write keep `old` = 0).
+__device__ __forceinline__ int wave_incl_sum(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+  return x;
+}
+
 __device__ __forceinline__ float wave_max(float x) {
   for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, kWave));
   return x;
@@ -292,10 +306,8 @@ __device__ int build_plan(const Params& p, int32_t* pre, int32_t* flat, int& chu
   };
   int64_t total = 0;
   for (int b0 = 0; b0 < p.B; b0 += kWave) {
-    int sum = (length(b0, b0 + lane) + kAlign - 1) / kAlign * kAlign;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, kWave);
-    total += sum;
+    const int padded = (length(b0, b0 + lane) + kAlign - 1) / kAlign * kAlign;
+    total += __builtin_amdgcn_readlane(wave_incl_sum(padded), kWave - 1);
   }
   // Chunks per call: target_units, doubled while that would need chunks above
   // chunk_max (a batch too long for target_units full-size chunks gets twice
@@ -317,28 +329,18 @@ __device__ int build_plan(const Params& p, int32_t* pre, int32_t* flat, int& chu
     const int b = b0 + lane;
     const int len = length(b0, b);
     const int padded = (len + kAlign - 1) / kAlign * kAlign;
-    int incl_f = padded;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const int y = __shfl_up(incl_f, off, kWave);
-      if (lane >= off) incl_f += y;
-    }
+    const int incl_f = wave_incl_sum(padded);
     const int fb = carry_f + incl_f - padded;
     const int n = len > 0 ? (fb + len - 1) / chunk - fb / chunk + 1 : 0;
-    int incl_u = n;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const int y = __shfl_up(incl_u, off, kWave);
-      if (lane >= off) incl_u += y;
-    }
+    const int incl_u = wave_incl_sum(n);
     if (b < p.B) {
       flat[b] = fb;
       pre[b] = min(carry_u + incl_u - n, p.u_max);  // the cap never binds with the host's u_max
     }
     if constexpr (kScores)
       if (blockIdx.x == 0 && b < p.B) p.lens_out[b] = len;
-    carry_f += __shfl(incl_f, kWave - 1, kWave);
-    carry_u += __shfl(incl_u, kWave - 1, kWave);
+    carry_f += __builtin_amdgcn_readlane(incl_f, kWave - 1);
+    carry_u += __builtin_amdgcn_readlane(incl_u, kWave - 1);
   }
   if (lane == 0) {
     flat[p.B] = carry_f;
