@@ -197,6 +197,7 @@ struct Params {
   int chunk_min, chunk_max;  // split size bounds in tokens (multiples of 32)
   int target_units;        // preferred number of sequence chunks per call
   int u_max;               // workspace capacity in units
+  int xcd_skew;            // automatic split: long/short chunk pairs for even/odd XCDs, in % (0: equal)
   int32_t* plan;           // [B+1] unit prefix offsets
   float* part_ml;          // [u_max, Hkv, G, 2]
   float* part_acc;         // [u_max, Hkv, G, D]
@@ -281,9 +282,48 @@ __device__ __forceinline__ HalfTile half_tile(const Params& p, int b, int start,
 // (flat[B] = stream length), pre[b] = first partial of sequence b (pre[B] =
 // total).  Workgroup 0 publishes pre for the reduce kernel.  Every workgroup
 // computes the same plan from the same lengths.  Returns the chunk count.
+// Chunk geometry.  The stream is cut into pairs of a long chunk (c_e tokens)
+// and a short one (c_o); c_e == c_o without an XCD skew.  Chunk j starts at
+// (j / 2) * (c_e + c_o) + (j odd ? c_e : 0).
+struct Split {
+  int c_e, c_o, pair;  // pair = c_e + c_o
+  int n;               // chunks in the call
+  int paired;          // items map even chunks to even XCDs (see item_of)
+};
+__device__ __forceinline__ int chunk_of(const Split& sp, int x) {
+  const int q = x / sp.pair;
+  return 2 * q + (x - q * sp.pair >= sp.c_e ? 1 : 0);
+}
+__device__ __forceinline__ int chunk_lo(const Split& sp, int j) { return (j >> 1) * sp.pair + (j & 1) * sp.c_e; }
+// (arithmetic, not a select: the compiler turns the select into a two-entry
+// table in scratch memory, whose loads are not known to be wave-uniform)
+__device__ __forceinline__ int chunk_len(const Split& sp, int j) { return sp.c_e + (j & 1) * (sp.c_o - sp.c_e); }
+
+// Work item w -> (chunk, head slot).  Workgroups are dealt to the 8 XCDs
+// round-robin (XCD = w mod 8 for the items of the first round), and on this
+// part the odd XCDs stream the same work 6-20 % slower than the even ones;
+// with a skew the long (even) chunks go to the even XCDs: item w = 8 m + x
+// takes pair index P = 4 m + x / 2 of its parity class, chunk 2 (P / NH) +
+// (x & 1), head slot P mod NH.  (A bijection when n is even and n NH is a
+// multiple of 8, which the plan ensures before setting `paired`.)
+__device__ __forceinline__ void item_of(const Split& sp, int64_t w, int NH, int& jc, int& hh) {
+  if (sp.paired) {
+    const int x = (int)(w & 7);
+    const int64_t P = (w >> 3) * 4 + (x >> 1);
+    const int64_t q = P / NH;
+    jc = (int)(2 * q) + (x & 1);
+    hh = (int)(P - q * NH);
+  } else {
+    jc = (int)(w / NH);
+    hh = (int)(w - (int64_t)jc * NH);
+  }
+}
+
+constexpr int kSkewMinChunk = 512;  // smallest split that gets the XCD skew (tokens)
+
 template <int kLayout, bool kScores>
-__device__ int build_plan(const Params& p, int32_t* pre, int32_t* flat, int& chunk_out, int& start0_out,
-                          int& len0_out) {
+__device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32_t* flat, int& start0_out,
+                                            int& len0_out) {
   constexpr int kAlign = kScores ? 128 : 32;
   const int lane = threadIdx.x;
   // Lengths of sequences lane, lane + 64, ...; the first block stays in a
@@ -322,7 +362,34 @@ __device__ int build_plan(const Params& p, int32_t* pre, int32_t* flat, int& chu
   else want = p.chunk_max;
   want = (want + kAlign - 1) / kAlign * kAlign;
   const int chunk = uniform((int)std::min<int64_t>(std::max<int64_t>(want, p.chunk_min), p.chunk_max));
-  chunk_out = chunk;
+  const int64_t cap = p.u_max - p.B - 1;  // chunks whose partials the workspace holds
+  Split sp;
+  sp.c_e = sp.c_o = chunk;
+  sp.pair = 2 * chunk;
+  sp.n = (int)((total + chunk - 1) / chunk);
+  sp.paired = 0;
+  const int NH = p.Hkv * p.n_hb;
+  if (p.xcd_skew > 0 && chunk >= kSkewMinChunk && total > 0) {
+    // long chunks (1 + skew %) for the even XCDs, short ones for the odd
+    // (short splits are latency-bound: there the longer chunks cost more)
+    int64_t ce = ((int64_t)chunk * (100 + p.xcd_skew) / 100 + kAlign - 1) / kAlign * kAlign;
+    ce = std::min<int64_t>(ce, p.chunk_max);
+    const int64_t co = 2 * (int64_t)chunk - ce;
+    const int64_t q = total / (2 * chunk), r = total - q * 2 * chunk;
+    int64_t n = 2 * q + (r > 0 ? 1 : 0) + (r > ce ? 1 : 0);
+    n += n & 1;  // even: a trailing chunk past the stream has no tokens
+    if (co >= kAlign && co < ce && n <= cap && (n * NH) % 8 == 0) {
+      sp.c_e = (int)ce;
+      sp.c_o = (int)co;
+      sp.n = (int)n;
+      sp.paired = 1;
+    }
+  }
+  sp.c_e = uniform(sp.c_e);
+  sp.c_o = uniform(sp.c_o);
+  sp.pair = sp.c_e + sp.c_o;
+  sp.n = uniform(sp.n);
+  sp.paired = uniform(sp.paired);
 
   int carry_f = 0, carry_u = 0;
   for (int b0 = 0; b0 < p.B; b0 += kWave) {
@@ -331,7 +398,7 @@ __device__ int build_plan(const Params& p, int32_t* pre, int32_t* flat, int& chu
     const int padded = (len + kAlign - 1) / kAlign * kAlign;
     const int incl_f = wave_incl_sum(padded);
     const int fb = carry_f + incl_f - padded;
-    const int n = len > 0 ? (fb + len - 1) / chunk - fb / chunk + 1 : 0;
+    const int n = len > 0 ? chunk_of(sp, fb + len - 1) - chunk_of(sp, fb) + 1 : 0;
     const int incl_u = wave_incl_sum(n);
     if (b < p.B) {
       flat[b] = fb;
@@ -350,7 +417,7 @@ __device__ int build_plan(const Params& p, int32_t* pre, int32_t* flat, int& chu
   if (blockIdx.x == 0) {
     for (int b = lane; b <= p.B; b += kWave) p.plan[b] = pre[b];
   }
-  return (carry_f + chunk - 1) / chunk;
+  return sp;
 }
 
 // Largest b with pre[b] <= u (u < pre[B]).
@@ -693,20 +760,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   const int g = lane >> 4;
   const int c = lane & 15;
 
-  int chunk, lane_start, lane_len;  // start and length of sequence `lane` (B <= 64)
-  const int n_chunks = build_plan<kLayout, kScores>(p, s_pre, s_flat, chunk, lane_start, lane_len);
+  int lane_start, lane_len;  // start and length of sequence `lane` (B <= 64)
+  const Split sp = build_plan<kLayout, kScores>(p, s_pre, s_flat, lane_start, lane_len);
   const int NH = p.Hkv * p.n_hb;
-  const int64_t W = (int64_t)n_chunks * NH;
+  const int64_t W = (int64_t)sp.n * NH;
   const float k_scale = kKvFp8 ? p.k_scale[0] : 1.0f;
   const float v_scale = kKvFp8 ? p.v_scale[0] : 1.0f;
   const float sscale = p.score_scale * k_scale;
 
   for (int64_t w = blockIdx.x; w < W; w += gridDim.x) {
-    const int jc = (int)(w / NH);
-    const int hh = (int)(w - (int64_t)jc * NH);
+    int jc, hh;
+    item_of(sp, w, NH, jc, hh);
     const int kvh = hh / p.n_hb;
     const int hb = hh - kvh * p.n_hb;
-    const int lo = jc * chunk, hi = lo + chunk;  // stream range of this chunk
+    const int lo = chunk_lo(sp, jc), hi = lo + chunk_len(sp, jc);  // stream range of this chunk
     for (int b = uniform(find_seq(s_flat, p.B, lo)); b < p.B; ++b) {
     const int fb = uniform(s_flat[b]);
     if (fb >= hi) break;
@@ -724,7 +791,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     un.t_begin = max(lo - fb, 0);
     un.t_end = min(hi - fb, un.len);
     if (un.t_end <= un.t_begin) continue;  // only padding of sequence b in this chunk
-    const int u = uniform(s_pre[b]) + (jc - fb / chunk);  // this segment's partial
+    const int u = uniform(s_pre[b]) + (jc - chunk_of(sp, fb));  // this segment's partial
     if (u >= p.u_max) continue;                          // (the host sizes u_max so this never holds)
     un.p_first = 0;
     un.win0 = un.win1 = 0;
@@ -1229,6 +1296,7 @@ struct Options {
   int chunk_tokens = 0;         // 0: automatic
   int waves_per_cu = 8;         // persistent grid size (workgroups per CU)
   int target_waves_per_cu = 4;  // automatic split: units of work per CU
+  int xcd_skew = 3;             // automatic split: extra share of the even XCDs, in % (see item_of)
 } g_opt;
 
 // Event triples recorded around decode calls while kernel timing is enabled.
@@ -1501,6 +1569,7 @@ int run_decode(const Common& c) {
   p.score_scale = c.sm_scale * kLog2e;
   p.B = c.B; p.Hkv = c.Hkv; p.G = G; p.n_hb = n_hb;
   p.chunk_min = sp.chunk_min; p.chunk_max = sp.chunk_max; p.target_units = sp.target_units;
+  p.xcd_skew = sp.chunk_min == sp.chunk_max ? 0 : g_opt.xcd_skew;  // not with a fixed split
   p.u_max = (int)u_max;
   uint8_t* ws = (uint8_t*)c.ws;
   p.plan = (int32_t*)(ws + wl.plan_off);
@@ -1660,6 +1729,11 @@ int fsk_set_option(const char* name, int64_t value) {
   if (!strcmp(name, "waves_per_cu")) {
     if (value < 1 || value > 64) return fail(FSK_ERR_INVALID, "waves_per_cu in [1, 64]");
     g_opt.waves_per_cu = (int)value;
+    return FSK_OK;
+  }
+  if (!strcmp(name, "xcd_skew")) {
+    if (value < 0 || value > 50) return fail(FSK_ERR_INVALID, "xcd_skew in [0, 50]");
+    g_opt.xcd_skew = (int)value;
     return FSK_OK;
   }
   if (!strcmp(name, "target_waves_per_cu")) {

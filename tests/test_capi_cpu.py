@@ -247,3 +247,33 @@ def test_fp8_kernels_keep_both_convert_halves():
             assert lo == hi, f"{name}: {ins} low {lo} vs high {hi}"
             checked += lo
     assert checked > 0
+
+
+def test_partial_kernels_keep_uniform_state_in_scalars():
+    """Every decode kernel keeps its work-plan state wave-uniform: no private
+    (scratch) memory and no readfirstlane loop around a buffer load, which
+    this compiler emits when a buffer resource is built from a value it
+    cannot prove uniform (a select lowered to a table in scratch, a value
+    leaving a loop whose bound came out of a wave shuffle)."""
+    from fasterkernels_amd import build
+    res = subprocess.run([build.hipcc(), *[f for f in build.compile_flags() if f not in ("-shared", "-fPIC")],
+                          "--cuda-device-only", "-S", build.SRC, "-o", "-"],
+                         capture_output=True, text=True, timeout=600)
+    assert res.returncode == 0, res.stderr[-2000:]
+    asm = res.stdout
+    names = re.findall(r"^(_ZN12_GLOBAL__N_114partial_kernel\w*):", asm, re.M)
+    assert len(names) >= 40
+    for name in names:
+        body = asm[asm.index(name + ":"):]
+        body = body[:body.index(".Lfunc_end")]
+        meta = asm[asm.index(".amdhsa_kernel " + name):][:4000]
+        scratch = int(re.search(r"amdhsa_private_segment_fixed_size (\d+)", meta).group(1))
+        waterfalls = len(re.findall(r"v_cmp_eq_u64_e32 vcc, s\[\d+:\d+\], v\[", body))
+        assert scratch == 0 and waterfalls == 0, (name, scratch, waterfalls)
+
+
+def test_xcd_skew_option(lib):
+    assert lib.fsk_set_option(b"xcd_skew", -1) == nat.FSK_ERR_INVALID
+    assert lib.fsk_set_option(b"xcd_skew", 51) == nat.FSK_ERR_INVALID
+    assert lib.fsk_set_option(b"xcd_skew", 0) == nat.FSK_OK
+    assert lib.fsk_set_option(b"xcd_skew", 3) == nat.FSK_OK

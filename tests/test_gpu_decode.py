@@ -371,3 +371,27 @@ def test_dense_batch_above_one_wave():
     out = dec.flash_decode_gqa_hf_dense_optimized(q.to(DEV), k.to(DEV), v.to(DEV), lt.to(DEV), st.to(DEV))
     ref = O.decode_dense(f64(q), f64(k), f64(v), lt.numpy(), st.numpy())
     assert_close(out, ref, 2e-3, 2e-3, "dense B=70")
+
+
+# ---------------------------------------------------------------------------
+# XCD skew: long and short chunks alternate and even chunks go to even XCDs
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("skew", [0, 3, 20])
+def test_xcd_skew_splits(skew):
+    from fasterkernels_amd import _native as nat
+    lens = [5000, 17000, 1, 9000, 12345, 20000, 700, 16000]  # total ~80K: 512+-token splits
+    wl = W.make("C3", overrides=dict(B=len(lens), lens=("list", lens), sinks=True), seed=61)
+    ref = oracle_for(wl)
+    nat.set_option("xcd_skew", skew)
+    try:
+        out = W.run(wl.to(DEV))
+        varlen = W.make("C1", overrides=dict(B=len(lens), lens=("list", lens)), seed=62)
+        vout, S = dec.flash_decode_gqa_varlen(*(t.to(DEV) for t in (varlen.q, varlen.k, varlen.v, varlen.cu_seqlens)),
+                                              return_block_scores=True)
+        torch.cuda.synchronize()
+    finally:
+        nat.set_option("xcd_skew", 3)
+    assert_close(out, ref, 2e-3, 2e-3, f"paged skew {skew}")
+    assert_close(vout, oracle_for(varlen), 2e-3, 2e-3, f"varlen skew {skew}")
+    want = O.block_scores_varlen(f64(varlen.q), f64(varlen.k), varlen.cu_seqlens.numpy(), n_blocks=S.shape[2])
+    assert_close(S, want, 2e-3, 2e-3, f"block scores skew {skew}")
