@@ -395,3 +395,28 @@ def test_xcd_skew_splits(skew):
     assert_close(vout, oracle_for(varlen), 2e-3, 2e-3, f"varlen skew {skew}")
     want = O.block_scores_varlen(f64(varlen.q), f64(varlen.k), varlen.cu_seqlens.numpy(), n_blocks=S.shape[2])
     assert_close(S, want, 2e-3, 2e-3, f"block scores skew {skew}")
+
+
+def test_hf_fp8_split_kv_long_cache():
+    """tests/test_triton_gqa_decode_fp8.py:58-74: caches of 6000 slots, every
+    length 5000, Q/K/V quantised per tensor, 8 splits."""
+    g = torch.Generator().manual_seed(42)
+    B, S = 4, 6000
+    q = torch.randn(B, 32, 128, generator=g)
+    k = torch.randn(B, 8, S, 128, generator=g)
+    v = torch.randn(B, 8, S, 128, generator=g)
+    lens = torch.full((B,), 5000, dtype=torch.int32)
+    q8, sq = dec.quantize_to_fp8(q)
+    k8, sk = dec.quantize_to_fp8(k)
+    v8, sv = dec.quantize_to_fp8(v)
+    dec.set_num_splits_fp8(8)
+    try:
+        out = dec.flash_decode_gqa_hf_fp8(q8.to(DEV), k8.to(DEV), v8.to(DEV), lens.to(DEV), sq.to(DEV), sk.to(DEV),
+                                          sv.to(DEV), torch.float16)
+        torch.cuda.synchronize()
+    finally:
+        dec.set_num_splits_fp8(1)
+    qd = (q8.to(torch.float32) * sq).to(torch.float16)
+    ref = O.decode_dense(f64(qd), k8.view(torch.uint8).numpy(), v8.view(torch.uint8).numpy(), lens.numpy(),
+                         k_scale=float(sk), v_scale=float(sv))
+    assert_close(out, ref, 1e-2, 0.0, "hf fp8 long cache, 8 splits")
