@@ -214,14 +214,23 @@ def test_varlen_fp8():
     run_and_check(wl, what="varlen fp8")
 
 
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("kv", ["f16", "bf16", "e4m3"])
+def test_varlen_head_dims(D, kv):
+    q = "bf16" if kv == "bf16" else "f16"
+    wl = W.make("C1", overrides=dict(B=3, D=D, lens=("list", [45, 530, 1]), kv=kv, q=q, out=q, sinks=True),
+                seed=31)
+    run_and_check(wl, what=f"varlen D={D} {kv}")
+
+
 # ---------------------------------------------------------------------------
 # dense (HF cache) and the fp8 reference API
 # ---------------------------------------------------------------------------
-def _dense_inputs(B, S, lens, starts, dtype, seed):
+def _dense_inputs(B, S, lens, starts, dtype, seed, D=128):
     g = torch.Generator().manual_seed(seed)
-    q = torch.randn(B, 32, 128, generator=g).to(dtype)
-    k = torch.randn(B, 8, S, 128, generator=g).to(dtype)
-    v = torch.randn(B, 8, S, 128, generator=g).to(dtype)
+    q = torch.randn(B, 32, D, generator=g).to(dtype)
+    k = torch.randn(B, 8, S, D, generator=g).to(dtype)
+    v = torch.randn(B, 8, S, D, generator=g).to(dtype)
     return q, k, v, torch.tensor(lens, dtype=torch.int32), (
         None if starts is None else torch.tensor(starts, dtype=torch.int32))
 
@@ -233,6 +242,16 @@ def test_dense_hf(num_splits):
                                                   starts.to(DEV), num_splits)
     ref = O.decode_dense(f64(q), f64(k), f64(v), lens.numpy(), starts.numpy())
     assert_close(out, ref, 2e-3, 2e-3, "dense")
+
+
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_dense_head_dims(D, dtype):
+    q, k, v, lens, starts = _dense_inputs(2, 900, [900, 37], [0, 5], dtype, 9, D=D)
+    out = dec.flash_decode_gqa_hf_dense_optimized(q.to(DEV), k.to(DEV), v.to(DEV), lens.to(DEV),
+                                                  starts.to(DEV), 4)
+    ref = O.decode_dense(f64(q), f64(k), f64(v), lens.numpy(), starts.numpy())
+    assert_close(out, ref, 2e-3, 2e-3, f"dense D={D} {dtype}")
 
 
 def test_hf_fp8_reference_api():
