@@ -290,8 +290,8 @@ struct Split {
   int n;               // chunks in the call
   int paired;          // items map even chunks to even XCDs (see item_of)
 };
-__device__ __forceinline__ int chunk_of(const Split& sp, int x) {
-  const int q = x / sp.pair;
+__device__ __forceinline__ int chunk_of(const Split& sp, int x) {  // x >= 0
+  const int q = (int)((uint32_t)x / (uint32_t)sp.pair);
   return 2 * q + (x - q * sp.pair >= sp.c_e ? 1 : 0);
 }
 __device__ __forceinline__ int chunk_lo(const Split& sp, int j) { return (j >> 1) * sp.pair + (j & 1) * sp.c_e; }
@@ -344,41 +344,45 @@ __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32
     }
     return b < p.B ? len : 0;
   };
-  int64_t total = 0;
+  // Stream length (the host bounds it below 2^31 - 4096, so the split
+  // arithmetic is unsigned 32-bit: the plan sits on every workgroup's
+  // critical path, and 64-bit division is a long software sequence).
+  uint32_t total = 0;
   for (int b0 = 0; b0 < p.B; b0 += kWave) {
     const int padded = (length(b0, b0 + lane) + kAlign - 1) / kAlign * kAlign;
-    total += __builtin_amdgcn_readlane(wave_incl_sum(padded), kWave - 1);
+    total += (uint32_t)__builtin_amdgcn_readlane(wave_incl_sum(padded), kWave - 1);
   }
+  total = (uint32_t)uniform((int)total);
+  auto cdiv = [](uint32_t a, uint32_t b) { return (a + b - 1) / b; };
   // Chunks per call: target_units, doubled while that would need chunks above
   // chunk_max (a batch too long for target_units full-size chunks gets twice
   // as many chunks rather than a count that leaves some CUs one item short).
-  int64_t target = p.target_units;
-  int64_t want = (total + target - 1) / target;
-  while (want > p.chunk_max && target < (1 << 24)) {
-    target *= 2;
-    want = (total + target - 1) / target;
-  }
-  if (p.u_max > p.B + 1) want = std::max<int64_t>(want, (total + (p.u_max - p.B - 1) - 1) / (p.u_max - p.B - 1));
-  else want = p.chunk_max;
+  // cdiv(total, t) > chunk_max exactly when t < cdiv(total, chunk_max).
+  const uint32_t chunk_max = (uint32_t)p.chunk_max;
+  const uint32_t t_need = cdiv(total, chunk_max);
+  uint32_t target = (uint32_t)p.target_units;
+  while (target < t_need && target < (1u << 24)) target *= 2;
+  uint32_t want = cdiv(total, target);
+  const uint32_t cap = p.u_max > p.B + 1 ? (uint32_t)(p.u_max - p.B - 1) : 0;  // chunks the workspace holds
+  want = cap > 0 ? max(want, cdiv(total, cap)) : chunk_max;
   want = (want + kAlign - 1) / kAlign * kAlign;
-  const int chunk = uniform((int)std::min<int64_t>(std::max<int64_t>(want, p.chunk_min), p.chunk_max));
-  const int64_t cap = p.u_max - p.B - 1;  // chunks whose partials the workspace holds
+  const uint32_t chunk = (uint32_t)uniform((int)min(max(want, (uint32_t)p.chunk_min), chunk_max));
   Split sp;
-  sp.c_e = sp.c_o = chunk;
-  sp.pair = 2 * chunk;
-  sp.n = (int)((total + chunk - 1) / chunk);
+  sp.c_e = sp.c_o = (int)chunk;
+  sp.pair = 2 * (int)chunk;
+  sp.n = (int)cdiv(total, chunk);
   sp.paired = 0;
   const int NH = p.Hkv * p.n_hb;
-  if (p.xcd_skew > 0 && chunk >= kSkewMinChunk && total > 0) {
+  if (p.xcd_skew > 0 && chunk >= (uint32_t)kSkewMinChunk && total > 0) {
     // long chunks (1 + skew %) for the even XCDs, short ones for the odd
     // (short splits are latency-bound: there the longer chunks cost more)
-    int64_t ce = ((int64_t)chunk * (100 + p.xcd_skew) / 100 + kAlign - 1) / kAlign * kAlign;
-    ce = std::min<int64_t>(ce, p.chunk_max);
-    const int64_t co = 2 * (int64_t)chunk - ce;
-    const int64_t q = total / (2 * chunk), r = total - q * 2 * chunk;
-    int64_t n = 2 * q + (r > 0 ? 1 : 0) + (r > ce ? 1 : 0);
+    uint32_t ce = (chunk * (uint32_t)(100 + p.xcd_skew) / 100 + kAlign - 1) / kAlign * kAlign;
+    ce = min(ce, chunk_max);
+    const uint32_t co = 2 * chunk - ce;
+    const uint32_t q = total / (2 * chunk), r = total - q * 2 * chunk;
+    uint32_t n = 2 * q + (r > 0 ? 1 : 0) + (r > ce ? 1 : 0);
     n += n & 1;  // even: a trailing chunk past the stream has no tokens
-    if (co >= kAlign && co < ce && n <= cap && (n * NH) % 8 == 0) {
+    if (co >= (uint32_t)kAlign && co < ce && n <= cap && ((int64_t)n * NH) % 8 == 0) {
       sp.c_e = (int)ce;
       sp.c_o = (int)co;
       sp.n = (int)n;
