@@ -954,6 +954,10 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) 
   const int b = blockIdx.y;
   const int kvh = h / p.G;
   const int hg = h - kvh * p.G;
+  // The sink and the sequence length are loaded with the unit range, not
+  // after the merge, so they cost no round trip of their own.
+  const float z = p.s_aux ? p.s_aux[h] : 0.f;
+  const int len_b = *(p.scores ? p.lens + b : p.plan + b);  // (no branch: one round trip with the plan)
   const int u0 = p.plan[b];
   const int n = p.plan[b + 1] - u0;
   const int64_t base = ((int64_t)u0 * p.Hkv + kvh) * p.G + hg;  // partial index of unit u0
@@ -1012,7 +1016,6 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) 
 
   float ref = M_use;  // reference point of den
   if (p.s_aux) {
-    const float z = p.s_aux[h];
     if (p.sink_mode == FSK_SINK_EXP) {
       // Extra logit z with a zero value vector (log2 domain: z * log2 e).
       const float z2 = z * kLog2e;
@@ -1029,7 +1032,7 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) 
   }
 
   if (p.scores) {
-    const int nvalid = (p.lens[b] + kScoreBlock - 1) / kScoreBlock;
+    const int nvalid = (len_b + kScoreBlock - 1) / kScoreBlock;
     const float inv = 1.f / den;
     const float* src = p.blk_max + ((int64_t)b * p.Hq + h) * p.nblk;
     uint8_t* dst = p.scores + ((int64_t)b * p.Hq + h) * p.nblk * (kOut == kF32 ? 4 : 2);
