@@ -114,6 +114,7 @@ def set_option(name: str, value: int) -> None:
 
 # (device, layout, batch, hq, hkv, d, kv_extent, page_size, chunk_tokens) -> bytes
 _WS_CACHE: dict = {}
+_WS_CACHE_MAX = 4096
 
 
 def workspace_bytes(layout: int, batch: int, hq: int, hkv: int, d: int, kv_extent: int,
@@ -133,6 +134,8 @@ def workspace_bytes(layout: int, batch: int, hq: int, hkv: int, d: int, kv_exten
     if n < 0:
         check(int(n))
     if device_index is not None:
+        if len(_WS_CACHE) >= _WS_CACHE_MAX:
+            _WS_CACHE.clear()  # (a varlen serving loop has a new total length every step)
         _WS_CACHE[key] = int(n)
     return int(n)
 

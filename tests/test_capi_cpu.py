@@ -67,6 +67,20 @@ def test_workspace_bytes(lib):
     assert f(nat.FSK_LAYOUT_PAGED, 4, 32, 8, 128, 2048, 16, 48) == nat.FSK_ERR_INVALID
 
 
+def test_workspace_size_cache_is_bounded(lib, monkeypatch):
+    """A varlen serving loop asks for a new total length every step: the
+    cached sizes must not grow without bound."""
+    monkeypatch.setattr(nat, "launch", lambda device_index, fn, *args: fn(*args))
+    nat._WS_CACHE.clear()
+    try:
+        sizes = {nat.workspace_bytes(nat.FSK_LAYOUT_VARLEN, 4, 32, 8, 128, 1000 + t, 16, 0, 0)
+                 for t in range(nat._WS_CACHE_MAX + 10)}
+        assert min(sizes) > 0
+        assert 0 < len(nat._WS_CACHE) <= nat._WS_CACHE_MAX
+    finally:
+        nat._WS_CACHE.clear()
+
+
 def paged_args(**kw):
     """A valid argument set for fsk_decode_paged (fake pointers), overridable."""
     a = dict(q=FAKE, q_sb=32 * 128, q_sh=128, k=FAKE, k_sp=8 * 16 * 128, k_sh=16 * 128, k_st=128,
