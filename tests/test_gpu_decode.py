@@ -168,6 +168,43 @@ def test_paged_head_dims(D, kv):
     run_and_check(wl, what=f"D={D} {kv}")
 
 
+@pytest.mark.parametrize("ps", [32, 64])
+@pytest.mark.parametrize("kv", ["f16", "e4m3"])
+def test_paged_page_sizes(ps, kv):
+    """Pages of 32 and 64 tokens (the C ABI takes any multiple of 16), scattered
+    through the pool, with lengths ending inside a page."""
+    g = torch.Generator().manual_seed(40 + ps)
+    B, Hq, Hkv, D = 3, 32, 8, 128
+    lens = [1, ps + 3, 40 * ps + 5]
+    nblk = [-(-L // ps) for L in lens]
+    P = sum(nblk) + 5
+    perm = torch.randperm(P, generator=g)
+    bt = torch.full((B, max(nblk) + 2), -1, dtype=torch.int32)
+    i = 0
+    for b, n in enumerate(nblk):
+        bt[b, :n] = perm[i:i + n]
+        i += n
+    q = torch.randn(B, Hq, D, generator=g).to(torch.float16)
+    k = torch.randn(P, Hkv, ps, D, generator=g)
+    v = torch.randn(P, Hkv, ps, D, generator=g)
+    seq_lens = torch.tensor(lens, dtype=torch.int32)
+    if kv == "e4m3":
+        kp, sk = dec.quantize_to_fp8(k)
+        vp, sv = dec.quantize_to_fp8(v)
+        out = dec.paged_flash_decode(q.to(DEV), kp.to(DEV), vp.to(DEV), bt.to(DEV), seq_lens.to(DEV), ps,
+                                     k_scale=sk.to(DEV), v_scale=sv.to(DEV))
+        ref = O.decode_paged(f64(q), kp.view(torch.uint8).numpy(), vp.view(torch.uint8).numpy(), bt.numpy(),
+                             lens, k_scale=float(sk), v_scale=float(sv))
+        tol = (1e-2, 0.0)
+    else:
+        kp, vp = k.to(torch.float16), v.to(torch.float16)
+        out = dec.paged_flash_decode(q.to(DEV), kp.to(DEV), vp.to(DEV), bt.to(DEV), seq_lens.to(DEV), ps)
+        ref = O.decode_paged(f64(q), f64(kp), f64(vp), bt.numpy(), lens)
+        tol = (2e-3, 2e-3)
+    torch.cuda.synchronize()
+    assert_close(out, ref, *tol, f"page_size={ps} {kv}")
+
+
 def test_paged_out_dtype_f32():
     wl = W.make("C3", overrides=dict(B=2, lens=("list", [100, 1000]), out="f32"), seed=17)
     run_and_check(wl, what="f32 out")
