@@ -110,6 +110,31 @@ def test_write_matches_oracle(src, pool, scaled):
     compare(vg, vo, pool, src, f"V {src}->{pool} scaled={scaled}")
 
 
+@pytest.mark.parametrize("ps", [32, 64])
+@pytest.mark.parametrize("src,pool,scaled", [("f16", "f16", False), ("bf16", "e4m3", True)])
+def test_write_page_sizes(ps, src, pool, scaled):
+    """Pages of 32 and 64 rows: slot s goes to page s // ps, row s % ps."""
+    gen = torch.Generator().manual_seed(12 + ps)
+    P, hkv, d, n = 9, 8, 128, 150
+    kx = source_values(n, hkv, d, src, gen)
+    vx = source_values(n, hkv, d, src, gen, spread=3.0)
+    slots = torch.randperm(P * ps, generator=gen)[:n].to(torch.int64)
+    kg, ko = sentinel_pools((P, hkv, ps, d), pool)
+    vg, vo = sentinel_pools((P, hkv, ps, d), pool)
+    kso, vso = (np.float32(0.05), np.float32(0.004)) if scaled else (None, None)
+    ks = None if kso is None else torch.tensor(kso, device=DEV)
+    vs = None if vso is None else torch.tensor(vso, device=DEV)
+    paged_kv_write(kx.to(DEV), vx.to(DEV), kg, vg, slots.to(DEV), k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    for x, o, sc in ((kx, ko, kso), (vx, vo, vso)):
+        if src == pool:
+            O.paged_store_rows(o.view(np.uint16), slots.numpy(), x.view(torch.int16).numpy().view(np.uint16))
+        else:
+            O.paged_write(o, slots.numpy(), x.float().numpy(), pool, sc)
+    compare(kg, ko, pool, src, f"K ps={ps} {src}->{pool}")
+    compare(vg, vo, pool, src, f"V ps={ps} {src}->{pool}")
+
+
 def _scales():
     fixed = [1.0, 0.5, 3.0, 1 / 3, 0.1, 0.0123, 4 / 448, 448 / 65504, 1e-3, 7.77e-5, 1e-8, 1e-30, 2.5e30,
              1.0000001, 0.99999994, 1e-40, 2.0 ** -126, 3.4e38]
