@@ -14,8 +14,8 @@ GB/s; ``us_per_step`` and ``pct_of_peak`` (of 8 TB/s) are reported beside it.
 the launch stream over the timed region.  ``cpu_baseline`` times the CPU
 oracle on a bounded sample of the same workload.
 
-Other workloads: ``--config C1..C5`` (decode configurations), ``--config
-W0..W2`` (the KV write path: a step is one store of a batch of new rows into
+Other workloads: ``--config C1..C5`` (decode configurations), ``--config M0b``
+(M0 with bf16 Q, KV and output), ``--config W0..W2`` (the KV write path: a step is one store of a batch of new rows into
 scattered pages; ``roofline`` is the write kernel).  ``--graph`` replays each
 decode step from a captured HIP graph; ``--block-scores`` also computes the
 pooled 128-token block scores.
@@ -38,7 +38,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="M0", help="workload name (decode: M0, C1..C5; KV write: W0..W2)")
+    ap.add_argument("--config", default="M0", help="workload name (decode: M0, M0b, C1..C5; KV write: W0..W2)")
     ap.add_argument("--sets", type=int, default=0, help="input sets to rotate (0: >= 4 and enough for > 1.1 GB)")
     ap.add_argument("--chunk", type=int, default=0, help="split size in tokens (0: library default)")
     ap.add_argument("--block-scores", action="store_true",
@@ -350,7 +350,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16" if base.k.dtype == torch.float16 else str(base.k.dtype).replace("torch.", ""),
+        "dtype": {torch.float16: "f16", torch.bfloat16: "bf16", torch.float8_e4m3fn: "e4m3"}[base.k.dtype],
         "data": f"synthetic N(0,1), generated on device, {n_sets} rotating input sets",
         "config": {
             "workload": f"{args.config}: {base.layout} GQA decode B={base.B} Hq={base.Hq} Hkv={base.Hkv} "

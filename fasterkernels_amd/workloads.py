@@ -39,6 +39,10 @@ CONFIGS = {
     # paged e4m3 KV + sinks, B=64, lognormal lengths
     "C5": dict(layout="paged", q="bf16", kv="e4m3", out="bf16", B=64, Hq=32, Hkv=8, D=128,
                lens=("lognormal", math.log(4096.0), 1.0, 16, 32768), sinks=True, seed=105),
+    # M0 in bf16 (the dtype PagedKVCache.from_config gives its pools,
+    # fskernels/paged_attn/paged_kv_cache.py:80)
+    "M0b": dict(layout="paged", q="bf16", kv="bf16", out="bf16", B=4, Hq=32, Hkv=8, D=128,
+                lens=("fixed", 32768), sinks=False, seed=100),
 }
 
 DTYPES = {"f16": torch.float16, "bf16": torch.bfloat16, "e4m3": torch.float8_e4m3fn,
