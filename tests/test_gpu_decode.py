@@ -333,6 +333,13 @@ def test_m0_full_size_parity_and_invariance():
     assert torch.equal(out_p.cpu(), out.cpu()[perm])
 
 
+def test_single_long_sequence():
+    """One 200003-token sequence spread over the whole GPU (about a hundred
+    splits merged for every head; the last page partly filled)."""
+    wl = W.make("M0", overrides=dict(B=1, lens=("list", [200003]), sinks=True), seed=7)
+    run_and_check(wl, what="B=1 L=200003")
+
+
 def test_c2_full_size_with_sinks():
     run_and_check(W.make("C2"), what="C2")
 
