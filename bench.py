@@ -10,13 +10,16 @@ rotated, with a footprint above 1.1 GB, beyond the 256 MB Infinity Cache.
 Prints one JSON line.  ``value`` is the achieved algorithmic HBM bandwidth of a
 whole step (valid K+V bytes + Q + output + block-table entries + lengths) in
 GB/s; ``us_per_step`` and ``pct_of_peak`` (of 8 TB/s) are reported beside it.
-``roofline`` is the split-KV partial kernel alone, timed with HIP events on
-the launch stream over the timed region.  ``cpu_baseline`` times the CPU
-oracle on a bounded sample of the same workload.
+``roofline`` is the split-KV partial kernel alone, timed with HIP events that
+its own dispatches stamp (hipExtLaunchKernel) over a second timed pass of the
+same steps that follows the timed steps: the timing costs host time per call,
+so the step timing runs without it.  ``cpu_baseline`` times the CPU oracle on
+a bounded sample of the same workload.
 
 Other workloads: ``--config C1..C5`` (decode configurations), ``--config M0b``
-(M0 with bf16 Q, KV and output), ``--config W0..W2`` (the KV write path: a step is one store of a batch of new rows into
-scattered pages; ``roofline`` is the write kernel).  ``--graph`` replays each
+(M0 with bf16 Q, KV and output), ``--config W0..W2`` (the KV write path: a
+step is one store of a batch of new rows into scattered pages; ``roofline`` is
+the write kernel).  ``--graph`` replays each
 decode step from a captured HIP graph; ``--block-scores`` also computes the
 pooled 128-token block scores.
 """
@@ -83,6 +86,11 @@ def read_traffic(path: str):
         if line.strip().startswith("bytes_per_launch:"):
             return int(float(line.split(":", 1)[1]))
     return None
+
+
+def kernel_timing_steps(steps: int) -> int:
+    """Length of the kernel-timing pass that follows the timed steps."""
+    return max(steps, 50)
 
 
 def cpu_baseline(wl, budget_s: float):
@@ -189,6 +197,7 @@ def bench_write(args):
     """The KV write path: one store of a batch of rows into scattered pages."""
     import torch
 
+    from fasterkernels_amd import _native as nat
     from fasterkernels_amd import workloads as W
 
     dev = torch.device("cuda", 0)
@@ -201,20 +210,20 @@ def bench_write(args):
     for i in range(args.warmup):
         W.run_write(sets[i % n_sets])
     torch.cuda.synchronize()
-    evs = []
     t0 = time.perf_counter()
     for i in range(args.steps):
-        rec = i % 8 == 0
-        if rec:
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
         W.run_write(sets[i % n_sets])
-        if rec:
-            b.record()
-            evs.append((a, b))
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    kern_ms = statistics.mean(a.elapsed_time(b) for a, b in evs)
+    # kernel duration: a second timed pass of the same steps, every write kernel
+    # stamped by its own dispatch (the hook costs host time, so it stays out of
+    # the step timing above)
+    nat.enable_kernel_timing(1)
+    for i in range(kernel_timing_steps(args.steps)):
+        W.run_write(sets[(args.steps + i) % n_sets])
+    kern_ms_sum, _, calls = nat.kernel_timing()
+    nat.enable_kernel_timing(0)
+    kern_ms = kern_ms_sum / max(calls, 1)
     ms_step = elapsed * 1e3 / args.steps
     gbs = alg_bytes / (ms_step / 1e3) / 1e9
     kern_gbs = alg_bytes / (kern_ms / 1e3) / 1e9
@@ -299,32 +308,32 @@ def main():
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    # Kernel durations: a second timed pass of the same steps, with timing on
+    # every call (the timing costs host time, so it stays out of the step
+    # timing above).
+    n_kt = kernel_timing_steps(args.steps)
     if args.graph:
-        # the library's event hook does not run inside a replay: time 1 replay in 8 with events
+        # the library's hook does not run inside a replay: HIP events around each replay
         evs = []
-        t0 = time.perf_counter()
-        for i in range(args.steps):
-            if i % 8 == 0:
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                a.record()
-                step(i)
-                b.record()
-                evs.append((a, b))
-            else:
-                step(i)
+        for i in range(n_kt):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            step(args.steps + i)
+            b.record()
+            evs.append((a, b))
         torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
         tot_ms = sum(a.elapsed_time(b) for a, b in evs)
         part_ms, calls = 0.0, len(evs)
     else:
-        # kernel durations: HIP events on one call in 8 of the timed region
-        nat.enable_kernel_timing(8)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for i in range(args.steps):
-            step(i)
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
+        # every partial and reduce kernel stamped by its own dispatch
+        nat.enable_kernel_timing(1)
+        for i in range(n_kt):
+            step(args.steps + i)
         part_ms, tot_ms, calls = nat.kernel_timing()
         nat.enable_kernel_timing(0)
 

@@ -23,6 +23,7 @@
 // exponential is a single v_exp_f32.
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 #include <math.h>
 #include <algorithm>
@@ -1306,7 +1307,8 @@ struct Options {
   int xcd_skew = 3;             // automatic split: extra share of the even XCDs, in % (see item_of)
 } g_opt;
 
-// Event triples recorded around decode calls while kernel timing is enabled.
+// Event triples of timed decode calls (the partial kernel's start and end and
+// the reduce kernel's end, stamped by the dispatches themselves).
 struct Timing {
   bool enabled = false;
   int every = 1;       // record on every n-th decode call
@@ -1331,11 +1333,24 @@ hipEvent_t timing_event() {
   return e;
 }
 
-void timing_mark(bool rec, hipStream_t s) {
-  if (!rec || !g_timing.enabled) return;
-  hipEvent_t e = timing_event();
-  if (e && hipEventRecord(e, s) == hipSuccess) g_timing.ev.push_back(e);
-  else g_timing.enabled = false;  // could not record: stop timing rather than mis-pair
+// Three events for this call if it is a timed one, else nulls.
+void timing_events(hipEvent_t ev[3]) {
+  ev[0] = ev[1] = ev[2] = nullptr;
+  if (!timing_this_call()) return;
+  for (int i = 0; i < 3; ++i) ev[i] = timing_event();
+  if (!ev[0] || !ev[1] || !ev[2]) {
+    for (int i = 0; i < 3; ++i)
+      if (ev[i]) g_timing.spare.push_back(ev[i]);
+    ev[0] = ev[1] = ev[2] = nullptr;
+    g_timing.enabled = false;  // could not create events: stop timing rather than mis-pair
+  }
+}
+
+// Keeps a launched call's events for fsk_kernel_timing, or returns them to
+// the spares when the call did not launch.
+void timing_keep(hipEvent_t ev[3], bool launched) {
+  if (!ev[0]) return;
+  for (int i = 0; i < 3; ++i) (launched ? g_timing.ev : g_timing.spare).push_back(ev[i]);
 }
 
 void timing_clear() {
@@ -1504,13 +1519,26 @@ int validate(const Common& c) {
   return FSK_OK;
 }
 
+// Stream of a launch, and the events (or null) that the dispatch itself
+// timestamps at the kernel's start and end (timing calls only).
+struct Launch {
+  hipStream_t s;
+  hipEvent_t start, stop;
+};
+
+template <typename K, typename... Args>
+void launch(K kernel, dim3 grid, dim3 block, uint32_t lds, const Launch& L, Args... args) {
+  if (L.start || L.stop) hipExtLaunchKernelGGL(kernel, grid, block, lds, L.s, L.start, L.stop, 0, args...);
+  else hipLaunchKernelGGL(kernel, grid, block, lds, L.s, args...);
+}
+
 template <int D, int kQ, int kKV, int kLayout, bool kScores>
-void launch_partial(const Params& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((partial_kernel<D, kQ, kKV, kLayout, kScores>), dim3(grid), dim3(64), 8 * (p.B + 1), s, p);
+void launch_partial(const Params& p, int grid, const Launch& s) {
+  launch(partial_kernel<D, kQ, kKV, kLayout, kScores>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p);
 }
 
 template <int D, int kLayout, bool kScores>
-int dispatch_qkv(const Params& p, int grid, int q_dt, int kv_dt, hipStream_t s) {
+int dispatch_qkv(const Params& p, int grid, int q_dt, int kv_dt, const Launch& s) {
   if (kv_dt == FSK_F16) launch_partial<D, kF16, kF16, kLayout, kScores>(p, grid, s);
   else if (kv_dt == FSK_BF16) launch_partial<D, kBF16, kBF16, kLayout, kScores>(p, grid, s);
   else if (q_dt == FSK_F16) launch_partial<D, kF16, kE4M3, kLayout, kScores>(p, grid, s);
@@ -1521,7 +1549,7 @@ int dispatch_qkv(const Params& p, int grid, int q_dt, int kv_dt, hipStream_t s) 
 }
 
 template <int D>
-int dispatch_layout(int layout, bool scores, const Params& p, int grid, int q_dt, int kv_dt, hipStream_t s) {
+int dispatch_layout(int layout, bool scores, const Params& p, int grid, int q_dt, int kv_dt, const Launch& s) {
   if (layout == FSK_LAYOUT_VARLEN)
     return scores ? dispatch_qkv<D, kVarlen, true>(p, grid, q_dt, kv_dt, s)
                   : dispatch_qkv<D, kVarlen, false>(p, grid, q_dt, kv_dt, s);
@@ -1532,12 +1560,12 @@ int dispatch_layout(int layout, bool scores, const Params& p, int grid, int q_dt
 }
 
 template <int D>
-void launch_reduce(const ReduceParams& rp, int B, int o_dt, hipStream_t s) {
+void launch_reduce(const ReduceParams& rp, int B, int o_dt, const Launch& s) {
   dim3 grid(rp.Hq, B);
   dim3 block(kReduceThreads);
-  if (o_dt == FSK_F16) hipLaunchKernelGGL((reduce_kernel<D, kF16>), grid, block, 0, s, rp);
-  else if (o_dt == FSK_BF16) hipLaunchKernelGGL((reduce_kernel<D, kBF16>), grid, block, 0, s, rp);
-  else hipLaunchKernelGGL((reduce_kernel<D, kF32>), grid, block, 0, s, rp);
+  if (o_dt == FSK_F16) launch(reduce_kernel<D, kF16>, grid, block, 0, s, rp);
+  else if (o_dt == FSK_BF16) launch(reduce_kernel<D, kBF16>, grid, block, 0, s, rp);
+  else launch(reduce_kernel<D, kF32>, grid, block, 0, s, rp);
 }
 
 int run_decode(const Common& c) {
@@ -1593,32 +1621,32 @@ int run_decode(const Common& c) {
   const int grid = (int)std::max<int64_t>(grid64, 1);
 
   (void)hipGetLastError();
-  const bool rec = timing_this_call();
-  timing_mark(rec, c.stream);
+  // Timed calls: the partial kernel's dispatch stamps its start and end, the
+  // reduce's its end (no separate event records around the launches).
+  hipEvent_t ev[3];
+  timing_events(ev);
   int rc;
   const bool sc = c.scores != nullptr;
-  if (c.D == 64) rc = dispatch_layout<64>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, c.stream);
-  else if (c.D == 128) rc = dispatch_layout<128>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, c.stream);
-  else rc = dispatch_layout<256>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, c.stream);
+  const Launch lp{c.stream, ev[0], ev[1]};
+  if (c.D == 64) rc = dispatch_layout<64>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
+  else if (c.D == 128) rc = dispatch_layout<128>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
+  else rc = dispatch_layout<256>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
   if (rc != FSK_OK) {
-    if (rec && g_timing.enabled && !g_timing.ev.empty()) {  // drop this call's first mark
-      g_timing.spare.push_back(g_timing.ev.back());
-      g_timing.ev.pop_back();
-    }
+    timing_keep(ev, false);
     return rc;
   }
 
-  timing_mark(rec, c.stream);
   ReduceParams rp;
   rp.plan = p.plan; rp.part_ml = p.part_ml; rp.part_acc = p.part_acc;
   rp.s_aux = c.s_aux; rp.sink_mode = c.sink_mode;
   rp.out = (uint8_t*)c.out; rp.o_sb = c.o_sb * oe; rp.o_sh = c.o_sh * oe;
   rp.Hq = c.Hq; rp.Hkv = c.Hkv; rp.G = G;
   rp.blk_max = p.blk_max; rp.lens = p.lens_out; rp.scores = (uint8_t*)c.scores; rp.nblk = c.nblk;
-  if (c.D == 64) launch_reduce<64>(rp, c.B, c.o_dt, c.stream);
-  else if (c.D == 128) launch_reduce<128>(rp, c.B, c.o_dt, c.stream);
-  else launch_reduce<256>(rp, c.B, c.o_dt, c.stream);
-  timing_mark(rec, c.stream);
+  const Launch lr{c.stream, nullptr, ev[2]};
+  if (c.D == 64) launch_reduce<64>(rp, c.B, c.o_dt, lr);
+  else if (c.D == 128) launch_reduce<128>(rp, c.B, c.o_dt, lr);
+  else launch_reduce<256>(rp, c.B, c.o_dt, lr);
+  timing_keep(ev, true);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(FSK_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(e));
   return FSK_OK;
@@ -1632,12 +1660,12 @@ FastDiv make_fastdiv(uint32_t d) {
 }
 
 template <int kSrc, int kPool, bool kScaled>
-void launch_write(const WriteParams& p, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((kv_write_kernel<kSrc, kPool, kScaled>), grid, dim3(kWriteThreads), 0, s, p);
+void launch_write(const WriteParams& p, dim3 grid, const Launch& s) {
+  launch(kv_write_kernel<kSrc, kPool, kScaled>, grid, dim3(kWriteThreads), 0, s, p);
 }
 
 template <int kSrc>
-void dispatch_write(const WriteParams& p, int pool_dt, bool scaled, dim3 grid, hipStream_t s) {
+void dispatch_write(const WriteParams& p, int pool_dt, bool scaled, dim3 grid, const Launch& s) {
   if (pool_dt == FSK_F16) launch_write<kSrc, kF16, false>(p, grid, s);
   else if (pool_dt == FSK_BF16) launch_write<kSrc, kBF16, false>(p, grid, s);
   else if (scaled) launch_write<kSrc, kE4M3, true>(p, grid, s);
@@ -1707,9 +1735,15 @@ int run_write(const WriteArgs& a) {
                                            (int64_t)device_cus() * FSK_WRITE_BLOCKS_PER_CU);
   const dim3 grid((unsigned)blocks, 2);
   (void)hipGetLastError();
-  if (a.src_dt == FSK_F16) dispatch_write<kF16>(p, a.pool_dt, scaled, grid, a.stream);
-  else if (a.src_dt == FSK_BF16) dispatch_write<kBF16>(p, a.pool_dt, scaled, grid, a.stream);
-  else dispatch_write<kF32>(p, a.pool_dt, scaled, grid, a.stream);
+  // Timed calls: the write kernel's dispatch stamps its start and end (the
+  // third event, recorded after it, keeps the record in triples).
+  hipEvent_t ev[3];
+  timing_events(ev);
+  const Launch lw{a.stream, ev[0], ev[1]};
+  if (a.src_dt == FSK_F16) dispatch_write<kF16>(p, a.pool_dt, scaled, grid, lw);
+  else if (a.src_dt == FSK_BF16) dispatch_write<kBF16>(p, a.pool_dt, scaled, grid, lw);
+  else dispatch_write<kF32>(p, a.pool_dt, scaled, grid, lw);
+  timing_keep(ev, !ev[0] || hipEventRecord(ev[2], a.stream) == hipSuccess);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(FSK_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(e));
   return FSK_OK;

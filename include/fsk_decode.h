@@ -251,12 +251,15 @@ FSK_API int fsk_fp8_decode_table(uint16_t *out, void *stream);
 FSK_API int fsk_set_option(const char *name, int64_t value);
 
 /* Profiling hook (no counterpart in the reference; used by the benchmark).
- * With every_n > 0, every n-th decode call records HIP events on its stream
- * before the split-KV partial kernel, between it and the reduce kernel, and
- * after the reduce kernel; every_n = 0 disables the hook.  Not for use under
- * HIP graph capture.  fsk_kernel_timing() waits for the recorded events,
- * returns the summed partial-kernel and partial+reduce milliseconds and the
- * number of recorded calls, and clears the record. */
+ * With every_n > 0, every n-th decode or write call launches its kernels with
+ * HIP events that the dispatches stamp (hipExtLaunchKernel): for a decode,
+ * the split-KV partial kernel's start and end and the reduce kernel's end;
+ * for a write, the write kernel's start and end.  every_n = 0 disables the
+ * hook.  A timed launch costs ~20 us of extra host time, so time steps with
+ * the hook off.  Not for use under HIP graph capture.  fsk_kernel_timing()
+ * waits for the recorded events, returns the summed first-kernel and
+ * first-kernel-start-to-last-kernel-end milliseconds and the number of
+ * recorded calls, and clears the record. */
 FSK_API int fsk_enable_kernel_timing(int every_n);
 FSK_API int fsk_kernel_timing(double *partial_ms, double *total_ms, int64_t *calls);
 
