@@ -11,7 +11,7 @@ Prints one JSON line.  ``value`` is the achieved algorithmic HBM bandwidth of a
 whole step (valid K+V bytes + Q + output + block-table entries + lengths) in
 GB/s; ``us_per_step`` and ``pct_of_peak`` (of 8 TB/s) are reported beside it.
 ``roofline`` is the split-KV partial kernel alone, timed with HIP events that
-its own dispatches stamp (hipExtLaunchKernel) on 1 call in 8 of a second
+its own dispatches stamp (hipExtLaunchKernel) on every call of a second
 pass of the same steps that follows the timed steps: the timing costs host
 time per call, so the step timing runs without it.  ``cpu_baseline`` times
 the CPU oracle on a bounded sample of the same workload.  The default
@@ -90,10 +90,12 @@ def read_traffic(path: str):
     return None
 
 
-# The kernel-timing pass stamps 1 call in KT_EVERY: a stamped launch leaves the
-# GPU idle for ~5-14 µs, and kernels that throttle under back-to-back load
-# (the quantising write) would read fast if every call were stamped.
-KT_EVERY = 8
+# The kernel-timing pass stamps every call.  A stamped dispatch starts after a
+# ~5-10 µs idle gap; a stamp on one call in several, right behind unstamped
+# ones, makes that kernel run ~2 µs longer (M0, rocprofv3), so a sparse
+# sample reads high.  Stamping every call reads within 0.5 % of the
+# back-to-back kernel durations rocprofv3 reports.
+KT_EVERY = 1
 
 
 def kernel_timing_steps(steps: int) -> int:
@@ -223,9 +225,9 @@ def bench_write(args):
         W.run_write(sets[i % n_sets])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    # kernel duration: a second timed pass of the same steps, 1 write kernel in
-    # KT_EVERY stamped by its own dispatch (the hook costs host time, so it
-    # stays out of the step timing above)
+    # kernel duration: a second timed pass of the same steps, the write kernels
+    # stamped by their own dispatches (the hook costs host time, so it stays
+    # out of the step timing above)
     nat.enable_kernel_timing(KT_EVERY)
     for i in range(kernel_timing_steps(args.steps)):
         W.run_write(sets[(args.steps + i) % n_sets])
@@ -321,9 +323,9 @@ def main():
         step(i)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    # Kernel durations: a second timed pass of the same steps, with timing on 1
-    # call in KT_EVERY (the timing costs host time, so it stays out of the step
-    # timing above).
+    # Kernel durations: a second timed pass of the same steps, with timing on
+    # the calls KT_EVERY selects (the timing costs host time, so it stays out
+    # of the step timing above).
     n_kt = kernel_timing_steps(args.steps)
     if args.graph:
         # the library's hook does not run inside a replay: HIP events around the replay
@@ -341,7 +343,7 @@ def main():
         tot_ms = sum(a.elapsed_time(b) for a, b in evs)
         part_ms, calls = 0.0, len(evs)
     else:
-        # the partial and reduce kernels of 1 call in KT_EVERY stamped by their dispatches
+        # the partial and reduce kernels stamped by their own dispatches
         nat.enable_kernel_timing(KT_EVERY)
         for i in range(n_kt):
             step(args.steps + i)
