@@ -280,8 +280,8 @@ def main():
         copy_calibration(args.copy_calibration)
         return
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only "
-                                   "(see DESIGN.md), so --gpus must be 1", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU (sharding the path across GPUs is a design "
+                                   "only), so --gpus must be 1", "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
 
