@@ -557,6 +557,28 @@ __device__ __forceinline__ HalfTile unit_half(const Params& p, const Unit& un, i
   return h;
 }
 
+// First tile of the unit's tile order.  On the varlen and dense layouts the
+// KV heads of a token row are 256-byte neighbours, and the waves of one chunk
+// (one per head) would read the same rows at the same moment: KV head h
+// starts at tile h * n / Hkv of its unit instead, and wraps round (C2: 84.7
+// -> 84.0 µs).  Paged units keep token order (their 4 KB page slabs stream
+// well in order; rotated, M0 83.0 -> 83.7 µs and C3 185 -> 188.7 µs), and so
+// do block scores (the running block maximum is stored when a block ends).
+template <int kLayout, bool kScores>
+__device__ __forceinline__ int tile_rotation(int kvh, int n_tiles, int Hkv) {
+  if constexpr (kScores || kLayout == kPaged) return 0;
+  return kvh * n_tiles / Hkv;
+}
+
+// Token position of the k-th tile of a unit of n tiles starting at t0 with
+// rotation rot (0 <= rot < n, or 0); tiles past the unit map to its end (an
+// empty tile).
+__device__ __forceinline__ int tile_pos(int k, int n, int rot, int t0, int t_end) {
+  int j = k + rot;
+  j -= j >= n ? n : 0;
+  return k < n ? t0 + 32 * j : t_end;
+}
+
 template <int D, int kKV, int kLayout>
 __device__ __forceinline__ void issue_tile(TileRegs<D, kKV>& T, uint32_t kstage_off, const Params& p,
                                            const Unit& un, int t, int g, int c) {
@@ -864,24 +886,27 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
       // tile is computed with exactly kDepth - 1 later tiles in flight (a
       // conditional issue would make the compiler wait for all loads).
       TR tiles[kDepth];
-      int t = un.t_begin;
+      const int n_tiles = (un.t_end - un.t_begin + 31) >> 5;
+      const int rot = uniform(tile_rotation<kLayout, kScores>(un.kvh, n_tiles, p.Hkv));
+      int k = 0;  // tiles computed so far
 #pragma unroll
       for (int s = 0; s < kDepth - 1; ++s)
-        issue_tile<D, kKV, kLayout>(tiles[s], s_kstage + s * 2 * TR::kHalfBytes, p, un, t + 32 * s, g, c);
+        issue_tile<D, kKV, kLayout>(tiles[s], s_kstage + s * 2 * TR::kHalfBytes, p, un,
+                                    tile_pos(s, n_tiles, rot, un.t_begin, un.t_end), g, c);
       bool done = false;
       while (!done) {
 #pragma unroll
         for (int s = 0; s < kDepth; ++s) {
           if (!done) {
-            const int tn = t + 32 * (kDepth - 1);
+            const int tn = tile_pos(k + kDepth - 1, n_tiles, rot, un.t_begin, un.t_end);
             const int sn = (s + kDepth - 1) % kDepth;
             issue_tile<D, kKV, kLayout>(tiles[sn], s_kstage + sn * 2 * TR::kHalfBytes, p, un, tn, g, c);
             wait_k_stage<TR::kLoads, kDepth>(kDepth - 1);
             const float mt = compute_tile<D, kQ, kKV>(tiles[s], s_kstage + s * 2 * TR::kHalfBytes, st, qop,
                                                       sscale, g, c);
-            if constexpr (kScores) bm.add(p, un, t, mt, head, head_ok, g);
-            t += 32;
-            done = t >= un.t_end;
+            if constexpr (kScores) bm.add(p, un, un.t_begin + 32 * k, mt, head, head_ok, g);
+            ++k;
+            done = k >= n_tiles;
           }
         }
       }
