@@ -483,3 +483,36 @@ def test_hf_fp8_split_kv_long_cache():
     ref = O.decode_dense(f64(qd), k8.view(torch.uint8).numpy(), v8.view(torch.uint8).numpy(), lens.numpy(),
                          k_scale=float(sk), v_scale=float(sv))
     assert_close(out, ref, 1e-2, 0.0, "hf fp8 long cache, 8 splits")
+
+
+# ---------------------------------------------------------------------------
+# randomized configurations
+# ---------------------------------------------------------------------------
+def _random_case(seed):
+    """A random decode configuration (layout, dtypes, head grouping, head dim,
+    batch, lengths with zeros and page-boundary values, sinks, split size)."""
+    r = np.random.default_rng(seed)
+    layout = ["M0", "C1"][r.integers(2)]           # paged / varlen
+    kv = ["f16", "bf16", "e4m3"][r.integers(3)]
+    q = "bf16" if kv == "bf16" else ["f16", "bf16"][r.integers(2)] if kv == "e4m3" else "f16"
+    out = [q, "f32"][r.integers(2)]
+    Hkv = int(r.choice([1, 2, 4, 8]))
+    G = int(r.choice([1, 2, 4, 7, 8, 16, 20]))
+    D = int(r.choice([64, 128, 256]))
+    B = int(r.integers(1, 9))
+    special = [0, 1, 15, 16, 17, 31, 32, 33, 127, 128, 129, 2047, 2048, 2049]
+    lens = [int(r.choice(special)) if r.random() < 0.4 else int(r.integers(1, 3000)) for _ in range(B)]
+    if all(L == 0 for L in lens):
+        lens[0] = 5
+    sinks = bool(r.integers(2))
+    chunk = int(r.choice([0, 0, 32, 96, 256, 2048]))
+    return layout, dict(B=B, Hq=G * Hkv, Hkv=Hkv, D=D, q=q, kv=kv, out=out, sinks=sinks,
+                        lens=("list", lens)), chunk
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_randomized_configurations(seed):
+    name, ov, chunk = _random_case(1000 + seed)
+    wl = W.make(name, overrides=ov, seed=seed)
+    # (an empty sequence without a sink is 0/0 in the reference: NaN on both sides)
+    run_and_check(wl, chunk_tokens=chunk, what=f"seed {seed}: {name} {ov} chunk={chunk}")
