@@ -516,3 +516,32 @@ def test_randomized_configurations(seed):
     wl = W.make(name, overrides=ov, seed=seed)
     # (an empty sequence without a sink is 0/0 in the reference: NaN on both sides)
     run_and_check(wl, chunk_tokens=chunk, what=f"seed {seed}: {name} {ov} chunk={chunk}")
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_randomized_dense_configurations(seed):
+    """Dense HF-cache layout: random batch, cache size, lengths, start offsets,
+    dtypes, head dim, head grouping, sinks and split hints."""
+    r = np.random.default_rng(2000 + seed)
+    B, Hkv = int(r.integers(1, 6)), int(r.choice([1, 2, 8]))
+    Hq = Hkv * int(r.choice([1, 4, 8, 12]))
+    D = int(r.choice([64, 128, 256]))
+    S = int(r.integers(1, 2500))
+    dtype = [torch.float16, torch.bfloat16][r.integers(2)]
+    lens = [int(r.integers(0, S + 1)) for _ in range(B)]
+    starts = [int(r.integers(0, L + 1)) if r.random() < 0.5 else 0 for L in lens]
+    if all(e - s == 0 for s, e in zip(starts, lens)):
+        lens[0], starts[0] = S, 0
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, D, generator=g).to(dtype)
+    k = torch.randn(B, Hkv, S, D, generator=g).to(dtype)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(dtype)
+    sinks = torch.randn(Hq, generator=g) if r.random() < 0.5 else None
+    splits = [None, 1, 3, 8][r.integers(4)]
+    lt = torch.tensor(lens, dtype=torch.int32)
+    st = torch.tensor(starts, dtype=torch.int32)
+    out = dec.flash_decode_gqa_hf_dense_optimized(q.to(DEV), k.to(DEV), v.to(DEV), lt.to(DEV), st.to(DEV), splits,
+                                                  s_aux=None if sinks is None else sinks.to(DEV))
+    torch.cuda.synchronize()
+    ref = O.decode_dense(f64(q), f64(k), f64(v), lens, starts, None if sinks is None else f64(sinks))
+    assert_close(out, ref, 2e-3, 2e-3, f"seed {seed}: B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} {dtype} splits={splits}")

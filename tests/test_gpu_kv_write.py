@@ -394,3 +394,38 @@ def test_write_replays_in_a_hip_graph():
         paged_kv_write(kx.to(DEV), vx.to(DEV), ref_k, ref_v, sl.to(DEV))
         torch.cuda.synchronize()
         assert torch.equal(kp, ref_k) and torch.equal(vp, ref_v), rep
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_randomized_writes(seed):
+    """Random pool sizes, page sizes, head counts, head dims, source / pool
+    types, scales and slot lists (with skipped and repeated-page slots)."""
+    r = np.random.default_rng(3000 + seed)
+    src = ["f16", "bf16", "f32"][r.integers(3)]
+    pool, scaled = [("f16", False), ("bf16", False), ("e4m3", False), ("e4m3", True)][r.integers(4)]
+    ps = int(r.choice([16, 32, 64]))
+    P, hkv, d = int(r.integers(1, 40)), int(r.choice([1, 2, 8])), int(r.choice([64, 128, 256]))
+    n = int(r.integers(1, min(P * ps, 300) + 1))
+    gen = torch.Generator().manual_seed(seed)
+    kx = source_values(n, hkv, d, src, gen)
+    vx = source_values(n, hkv, d, src, gen, spread=3.0)
+    slots = torch.randperm(P * ps, generator=gen)[:n].to(torch.int64)
+    if n > 3:
+        slots[int(r.integers(n))] = -1   # a skipped token
+    kg, ko = sentinel_pools((P, hkv, ps, d), pool)
+    vg, vo = sentinel_pools((P, hkv, ps, d), pool)
+    kso = vso = None
+    if scaled:
+        kso, vso = np.float32(r.uniform(1e-3, 1.0)), np.float32(r.uniform(1e-3, 1.0))
+    ks = None if kso is None else torch.tensor(kso, device=DEV)
+    vs = None if vso is None else torch.tensor(vso, device=DEV)
+    paged_kv_write(kx.to(DEV), vx.to(DEV), kg, vg, slots.to(DEV), k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    for x, o, sc in ((kx, ko, kso), (vx, vo, vso)):
+        if src == pool:
+            O.paged_store_rows(o.view(np.uint16), slots.numpy(), x.view(torch.int16).numpy().view(np.uint16))
+        else:
+            O.paged_write(o, slots.numpy(), x.float().numpy(), pool, sc)
+    what = f"seed {seed}: {src}->{pool} scaled={scaled} P={P} ps={ps} hkv={hkv} d={d} n={n}"
+    compare(kg, ko, pool, src, "K " + what)
+    compare(vg, vo, pool, src, "V " + what)
