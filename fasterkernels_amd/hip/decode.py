@@ -190,11 +190,12 @@ def flash_decode_gqa_varlen(q, k_varlen, v_varlen, cu_seqlens_k, s_aux=None, *,
         nbytes += nat.score_workspace_bytes(B, Hq, nblk)
     ws = _workspace(nbytes, dev)
     lib = nat.load()
-    args = (q.data_ptr(), q.stride(0), q.stride(1),
-            k.data_ptr(), k.stride(0), k.stride(1),
-            v.data_ptr(), v.stride(0), v.stride(1),
+    qs, kst, vst, os_ = q.stride(), k.stride(), v.stride(), out.stride()  # (one call each)
+    args = (q.data_ptr(), qs[0], qs[1],
+            k.data_ptr(), kst[0], kst[1],
+            v.data_ptr(), vst[0], vst[1],
             cu.data_ptr(), T, nat.ptr(sinks), _sink_mode(sink_mode), ksp, vsp,
-            out.data_ptr(), out.stride(0), out.stride(1),
+            out.data_ptr(), os_[0], os_[1],
             B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_varlen"),
             _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens)
     if scores is None:
@@ -250,13 +251,14 @@ def _dense(q, k_cache, v_cache, cache_lens, start_k_offsets, num_splits, *, q_sc
     nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_DENSE, B, Hq, Hkv, D, S, 16, chunk_tokens, dev.index)
     ws = _workspace(nbytes, dev)
     lib = nat.load()
+    qs, kst, vst, os_ = q.stride(), k.stride(), v.stride(), out.stride()
     st = nat.launch(
         dev.index, lib.fsk_decode_dense,
-        q.data_ptr(), q.stride(0), q.stride(1),
-        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
-        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), S,
+        q.data_ptr(), qs[0], qs[1],
+        k.data_ptr(), kst[0], kst[1], kst[2],
+        v.data_ptr(), vst[0], vst[1], vst[2], S,
         lens.data_ptr(), nat.ptr(starts), nat.ptr(sinks), _sink_mode(sink_mode), qsp, ksp, vsp,
-        out.data_ptr(), out.stride(0), out.stride(1),
+        out.data_ptr(), os_[0], os_[1],
         B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_cache"),
         _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens,
         nat.stream_handle(dev))
@@ -333,8 +335,10 @@ def paged_flash_decode(q, k_pool, v_pool, block_table, seq_lens, page_size, *, s
     if block_table.dim() != 2 or block_table.shape[0] < B:
         raise ValueError("block_table must be [batch, max_blocks]")
     bt = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
-    if bt.stride(1) != 1:
+    bts = bt.stride()
+    if bts[1] != 1:
         bt = bt.contiguous()
+        bts = bt.stride()
     lens = _int32(seq_lens, "seq_lens", dev)
     if lens.numel() < B:
         raise ValueError("seq_lens must have one entry per sequence")
@@ -351,12 +355,13 @@ def paged_flash_decode(q, k_pool, v_pool, block_table, seq_lens, page_size, *, s
         nbytes += nat.score_workspace_bytes(B, Hq, nblk)
     ws = _workspace(nbytes, dev)
     lib = nat.load()
-    args = (q.data_ptr(), q.stride(0), q.stride(1),
-            k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
-            v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
-            bt.data_ptr(), bt.stride(0), max_blocks, lens.data_ptr(), P, PS,
+    qs, kst, vst, os_ = q.stride(), k.stride(), v.stride(), out.stride()
+    args = (q.data_ptr(), qs[0], qs[1],
+            k.data_ptr(), kst[0], kst[1], kst[2],
+            v.data_ptr(), vst[0], vst[1], vst[2],
+            bt.data_ptr(), bts[0], max_blocks, lens.data_ptr(), P, PS,
             nat.ptr(sinks), _sink_mode(sink_mode), ksp, vsp,
-            out.data_ptr(), out.stride(0), out.stride(1),
+            out.data_ptr(), os_[0], os_[1],
             B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_pool"),
             _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens)
     if scores is None:

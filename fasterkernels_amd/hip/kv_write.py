@@ -96,12 +96,13 @@ def paged_kv_write(k: torch.Tensor, v: torch.Tensor, k_pool: torch.Tensor, v_poo
         bt_ptr, bt_numel = block_table.data_ptr(), block_table.numel()
         upd_ptr, n_upd = bt_updates.data_ptr(), bt_updates.shape[0]
     lib = nat.load()
+    ks_, vs_, kps, vps = k.stride(), v.stride(), k_pool.stride(), v_pool.stride()  # (one call each)
     st = nat.launch(
         dev.index, lib.fsk_paged_write,
-        k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
+        k.data_ptr(), ks_[0], ks_[1], v.data_ptr(), vs_[0], vs_[1],
         slot_mapping.data_ptr(), n,
-        k_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
-        v_pool.data_ptr(), v_pool.stride(0), v_pool.stride(1), v_pool.stride(2),
+        k_pool.data_ptr(), kps[0], kps[1], kps[2],
+        v_pool.data_ptr(), vps[0], vps[1], vps[2],
         P, ps, Hkv, D, nat.DTYPE_CODES[k.dtype], nat.DTYPE_CODES[k_pool.dtype],
         nat.ptr(ks), nat.ptr(vs), bt_ptr, bt_numel, upd_ptr, n_upd, nat.stream_handle(dev))
     nat.check(st)
