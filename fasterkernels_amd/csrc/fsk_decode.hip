@@ -92,11 +92,6 @@ __device__ __forceinline__ int wave_incl_sum(int x) {
   return x;
 }
 
-__device__ __forceinline__ float wave_max(float x) {
-  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, kWave));
-  return x;
-}
-
 // e4m3fn -> f16 / bf16, two codes per call (bytes 0,1 or 2,3 of `w`).  Both
 // conversions are exact: every e4m3 value is representable in f16 and bf16.
 template <bool kToBf16, bool kHi>
