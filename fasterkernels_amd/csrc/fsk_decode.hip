@@ -1484,8 +1484,15 @@ int64_t score_ws_bytes(int B, int Hq, int nblk) {
   return align256((int64_t)B * Hq * nblk * 4) + align256(4 * (int64_t)B);
 }
 
+// Bounds on batch and query heads: keep every size product (batch x heads x
+// blocks or units x 4 bytes) inside int64.
+constexpr int kMaxBatch = 16384;
+constexpr int kMaxQHeads = 1 << 16;
+constexpr int64_t kMaxStride = (int64_t)1 << 40;
+
 int validate(const Common& c) {
   if (c.B < 0 || c.Hq <= 0 || c.Hkv <= 0) return fail(FSK_ERR_INVALID, "batch/heads must be positive");
+  if (c.Hq > kMaxQHeads) return fail(FSK_ERR_UNSUPPORTED, "num_q_heads above 65536");
   if (c.Hq % c.Hkv != 0) return fail(FSK_ERR_INVALID, "num_q_heads must be a multiple of num_kv_heads");
   if (c.D != 64 && c.D != 128 && c.D != 256) return fail(FSK_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256");
   // An empty varlen/dense KV (extent 0: every sequence empty) reads no row, so
@@ -1505,6 +1512,12 @@ int validate(const Common& c) {
   }
   if (c.q_dt == FSK_E4M3 && !c.q_scale) return fail(FSK_ERR_INVALID, "e4m3 q needs q_scale");
   if (!(c.sm_scale == c.sm_scale) || !std::isfinite(c.sm_scale)) return fail(FSK_ERR_INVALID, "sm_scale must be finite");
+  // Strides (elements) are non-negative and below 2^40, so the byte products
+  // below stay inside int64.
+  for (const int64_t st : {c.q_sb, c.q_sh, c.k_s0, c.k_sh, c.k_st, c.v_s0, c.v_sh, c.v_st, c.o_sb, c.o_sh, c.bt_sb}) {
+    if (st < 0) return fail(FSK_ERR_INVALID, "negative stride");
+    if (st >= kMaxStride) return fail(FSK_ERR_UNSUPPORTED, "stride above 2^40 elements");
+  }
   const int qe = elem_bytes(c.q_dt), ke = elem_bytes(c.kv_dt), oe = elem_bytes(c.o_dt);
   // Row starts must be 16-byte aligned (8 for e4m3 q) for the vector loads.
   const int qa = (c.q_dt == FSK_E4M3) ? 8 : 16;
@@ -1513,8 +1526,6 @@ int validate(const Common& c) {
       (c.v_sh * ke) % 16 || (c.k_s0 * ke) % 16 || (c.v_s0 * ke) % 16)
     return fail(FSK_ERR_INVALID, "k/v rows must be 16-byte aligned");
   if (c.k_st < c.D || c.v_st < c.D) return fail(FSK_ERR_INVALID, "k/v token stride must be >= head_dim");
-  if (c.q_sb < 0 || c.q_sh < 0 || c.k_s0 < 0 || c.k_sh < 0 || c.v_s0 < 0 || c.v_sh < 0 || c.o_sb < 0 || c.o_sh < 0)
-    return fail(FSK_ERR_INVALID, "negative stride");
   if ((c.k_st * ke) * 16 >= (int64_t)1 << 31 || (c.v_st * ke) * 16 >= (int64_t)1 << 31)
     return fail(FSK_ERR_UNSUPPORTED, "k/v token stride too large");
   if (!aligned(c.out, 4 * oe) || (c.o_sb * oe) % (4 * oe) || (c.o_sh * oe) % (4 * oe))
@@ -1527,7 +1538,7 @@ int validate(const Common& c) {
     if (c.max_blocks < 0 || c.bt_sb < c.max_blocks) return fail(FSK_ERR_INVALID, "bad block_table shape");
     if ((int64_t)c.max_blocks * c.page_size >= ((int64_t)1 << 31)) return fail(FSK_ERR_UNSUPPORTED, "block table too wide");
   }
-  if (c.B > 16384) return fail(FSK_ERR_UNSUPPORTED, "batch above 16384");
+  if (c.B > kMaxBatch) return fail(FSK_ERR_UNSUPPORTED, "batch above 16384");
   if (stream_bound(c.layout, c.B, c.kv_extent, c.page_size > 0 ? c.page_size : 16) >= ((int64_t)1 << 31) - 4096)
     return fail(FSK_ERR_UNSUPPORTED, "total token extent of the batch above 2^31");
   if (c.scores) {
@@ -1704,7 +1715,9 @@ struct WriteArgs {
 
 int run_write(const WriteArgs& a) {
   if (a.n < 0 || a.n_upd < 0) return fail(FSK_ERR_INVALID, "negative count");
+  if (a.n >= ((int64_t)1 << 31)) return fail(FSK_ERR_UNSUPPORTED, "batch too large for one call");
   if (a.Hkv <= 0 || a.D <= 0) return fail(FSK_ERR_INVALID, "num_kv_heads and head_dim must be positive");
+  if (a.Hkv > kMaxQHeads) return fail(FSK_ERR_UNSUPPORTED, "num_kv_heads above 65536");
   if (a.D % 8 || a.D > 8 * kWriteThreads) return fail(FSK_ERR_UNSUPPORTED, "head_dim must be a multiple of 8, at most 2048");
   if (a.page_size <= 0 || a.num_pages <= 0) return fail(FSK_ERR_INVALID, "page_size and num_pages must be positive");
   if (a.src_dt != FSK_F16 && a.src_dt != FSK_BF16 && a.src_dt != FSK_F32)
@@ -1720,8 +1733,10 @@ int run_write(const WriteArgs& a) {
   const int pa = pe == 1 ? 8 : 16;
   for (int kv = 0; kv < 2; ++kv) {
     if (a.n > 0 && (!a.src[kv] || !a.pool[kv])) return fail(FSK_ERR_INVALID, "null tensor pointer");
-    if (a.s_st[kv] < 0 || a.s_sh[kv] < 0 || a.p_sp[kv] < 0 || a.p_sh[kv] < 0 || a.p_st[kv] < 0)
-      return fail(FSK_ERR_INVALID, "negative stride");
+    for (const int64_t st : {a.s_st[kv], a.s_sh[kv], a.p_sp[kv], a.p_sh[kv], a.p_st[kv]}) {
+      if (st < 0) return fail(FSK_ERR_INVALID, "negative stride");
+      if (st >= kMaxStride) return fail(FSK_ERR_UNSUPPORTED, "stride above 2^40 elements");
+    }
     if (!aligned(a.src[kv], 16) || (a.s_st[kv] * se) % 16 || (a.s_sh[kv] * se) % 16)
       return fail(FSK_ERR_INVALID, "new K/V rows must be 16-byte aligned");
     if (!aligned(a.pool[kv], pa) || (a.p_sp[kv] * pe) % pa || (a.p_sh[kv] * pe) % pa || (a.p_st[kv] * pe) % pa)
@@ -1729,8 +1744,8 @@ int run_write(const WriteArgs& a) {
     if (a.page_size > 1 && a.p_st[kv] < a.D) return fail(FSK_ERR_INVALID, "pool row stride must be >= head_dim");
   }
   if (a.n && a.slots == nullptr) return fail(FSK_ERR_INVALID, "null slot_mapping");
-  const int64_t total = a.n * a.Hkv * (int64_t)(a.D / 8);
-  if (a.n >= ((int64_t)1 << 31) || total >= ((int64_t)1 << 31)) return fail(FSK_ERR_UNSUPPORTED, "batch too large for one call");
+  const int64_t total = a.n * a.Hkv * (int64_t)(a.D / 8);  // (< 2^55 with the bounds above)
+  if (total >= ((int64_t)1 << 31)) return fail(FSK_ERR_UNSUPPORTED, "batch too large for one call");
   if ((int64_t)a.num_pages * a.page_size >= ((int64_t)1 << 31)) return fail(FSK_ERR_UNSUPPORTED, "pool above 2^31 slots");
   if (total == 0 && a.n_upd == 0) return FSK_OK;
 
@@ -1846,6 +1861,8 @@ int64_t fsk_workspace_bytes(int layout, int batch, int num_q_heads, int num_kv_h
   if (layout < 0 || layout > 2) return fail(FSK_ERR_INVALID, "bad layout");
   if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads || kv_extent < 0)
     return fail(FSK_ERR_INVALID, "bad shape");
+  if (num_q_heads > kMaxQHeads) return fail(FSK_ERR_UNSUPPORTED, "num_q_heads above 65536");
+  if (batch > kMaxBatch) return fail(FSK_ERR_UNSUPPORTED, "batch above 16384");
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return fail(FSK_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256");
   if (layout == FSK_LAYOUT_PAGED && (page_size <= 0 || page_size % 16)) return fail(FSK_ERR_UNSUPPORTED, "page_size must be a positive multiple of 16");
   if (chunk_tokens < 0 || chunk_tokens % 32) return fail(FSK_ERR_INVALID, "chunk_tokens: 0 or a multiple of 32");
@@ -1860,6 +1877,8 @@ int64_t fsk_workspace_bytes(int layout, int batch, int num_q_heads, int num_kv_h
 int64_t fsk_score_workspace_bytes(int batch, int num_q_heads, int score_blocks) {
   if (batch < 0 || num_q_heads <= 0 || score_blocks <= 0 || score_blocks > (1 << 24))
     return fail(FSK_ERR_INVALID, "bad shape");
+  if (num_q_heads > kMaxQHeads) return fail(FSK_ERR_UNSUPPORTED, "num_q_heads above 65536");
+  if (batch > kMaxBatch) return fail(FSK_ERR_UNSUPPORTED, "batch above 16384");
   return score_ws_bytes(batch > 0 ? batch : 1, num_q_heads, score_blocks);
 }
 
@@ -1993,6 +2012,11 @@ int fsk_paged_gather(const void* pool, int64_t stride_p, int64_t stride_h, int64
     return fail(FSK_ERR_INVALID, "bad shape");
   if (page_size <= 0 || page_size % 16) return fail(FSK_ERR_UNSUPPORTED, "page_size must be a positive multiple of 16");
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return fail(FSK_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256");
+  if (batch > kMaxBatch || num_kv_heads > kMaxQHeads) return fail(FSK_ERR_UNSUPPORTED, "batch or num_kv_heads too large");
+  for (const int64_t st : {stride_p, stride_h, stride_t, bt_stride_b}) {
+    if (st < 0) return fail(FSK_ERR_INVALID, "negative stride");
+    if (st >= kMaxStride) return fail(FSK_ERR_UNSUPPORTED, "stride above 2^40 elements");
+  }
   const int e = elem_bytes(dtype);
   if (e != 1 && e != 2) return fail(FSK_ERR_UNSUPPORTED, "dtype must be f16, bf16 or e4m3");
   if (!aligned(pool, 16) || !aligned(out, 16) || (stride_p * e) % 16 || (stride_h * e) % 16 || (stride_t * e) % 16 ||

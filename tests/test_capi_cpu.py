@@ -67,6 +67,14 @@ def test_workspace_bytes(lib):
     assert f(nat.FSK_LAYOUT_PAGED, 4, 32, 8, 128, 2048, 16, 48) == nat.FSK_ERR_INVALID
 
 
+def test_workspace_sizes_reject_overflowing_shapes(lib):
+    assert lib.fsk_score_workspace_bytes(1 << 30, 1 << 16, 1 << 24) == nat.FSK_ERR_UNSUPPORTED
+    assert lib.fsk_score_workspace_bytes(4, 1 << 20, 256) == nat.FSK_ERR_UNSUPPORTED
+    assert lib.fsk_score_workspace_bytes(16384, 1 << 16, 1 << 24) > 0
+    assert lib.fsk_workspace_bytes(nat.FSK_LAYOUT_PAGED, 4, 1 << 20, 8, 128, 2048, 16, 0) == nat.FSK_ERR_UNSUPPORTED
+    assert lib.fsk_workspace_bytes(nat.FSK_LAYOUT_PAGED, 1 << 20, 32, 8, 128, 2048, 16, 0) == nat.FSK_ERR_UNSUPPORTED
+
+
 def test_workspace_size_cache_is_bounded(lib, monkeypatch):
     """A varlen serving loop asks for a new total length every step: the
     cached sizes must not grow without bound."""
@@ -114,6 +122,14 @@ def paged_args(**kw):
     (dict(chunk=48), nat.FSK_ERR_INVALID),
     (dict(chunk=4096), nat.FSK_ERR_UNSUPPORTED),
     (dict(scale=float("nan")), nat.FSK_ERR_INVALID),
+    # size arithmetic stays inside int64: strides, heads and batch are bounded
+    (dict(q_sb=(1 << 62) + 8), nat.FSK_ERR_UNSUPPORTED),
+    (dict(k_sp=1 << 40), nat.FSK_ERR_UNSUPPORTED),
+    (dict(bt_sb=(1 << 63) - 1), nat.FSK_ERR_UNSUPPORTED),
+    (dict(o_sh=-128), nat.FSK_ERR_INVALID),
+    (dict(k_st=-128), nat.FSK_ERR_INVALID),
+    (dict(Hq=1 << 17, Hkv=8), nat.FSK_ERR_UNSUPPORTED),
+    (dict(B=16385), nat.FSK_ERR_UNSUPPORTED),
 ])
 def test_paged_validation(lib, override, code):
     assert lib.fsk_decode_paged(*paged_args(**override)) == code
@@ -179,6 +195,10 @@ def write_args(**kw):
     (dict(kp_sh=-16), nat.FSK_ERR_INVALID),
     (dict(n_upd=2, upd=FAKE), nat.FSK_ERR_INVALID),            # updates without a block table
     (dict(P=1 << 28, ps=16), nat.FSK_ERR_UNSUPPORTED),         # 2^32 slots
+    (dict(n=1 << 40), nat.FSK_ERR_UNSUPPORTED),                # size products stay inside int64
+    (dict(k_st=(1 << 62) + 8), nat.FSK_ERR_UNSUPPORTED),
+    (dict(kp_sp=1 << 40), nat.FSK_ERR_UNSUPPORTED),
+    (dict(Hkv=1 << 20), nat.FSK_ERR_UNSUPPORTED),
 ])
 def test_paged_write_validation(lib, override, code):
     assert lib.fsk_paged_write(*write_args(**override)) == code
