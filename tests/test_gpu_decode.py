@@ -545,3 +545,19 @@ def test_randomized_dense_configurations(seed):
     torch.cuda.synchronize()
     ref = O.decode_dense(f64(q), f64(k), f64(v), lens, starts, None if sinks is None else f64(sinks))
     assert_close(out, ref, 2e-3, 2e-3, f"seed {seed}: B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} {dtype} splits={splits}")
+
+
+@pytest.mark.parametrize("layout", ["M0", "C1"])
+@pytest.mark.parametrize("sink_scale", [0.0, 60.0])
+def test_large_logits_and_sinks(layout, sink_scale):
+    """Scores of several hundred (q and k scaled by 6: logits ~ N(0, 36^2) /
+    sqrt(D) with outliers) and sinks of +-60: the online softmax and the sink
+    fold must neither overflow nor lose the dominant terms."""
+    wl = W.make(layout, overrides=dict(B=3, lens=("list", [1, 700, 3000]), sinks=True), seed=77)
+    wl.q = (wl.q.float() * 6).to(wl.q.dtype)
+    wl.k = (wl.k.float() * 6).to(wl.k.dtype)
+    wl.s_aux = wl.s_aux * sink_scale
+    for mode in ("exp", "linear"):
+        ref = oracle_for(wl, mode)
+        assert np.isfinite(ref).all()
+        run_and_check(wl, sink_mode=mode, what=f"{layout} large logits, sinks x{sink_scale}, {mode}")
