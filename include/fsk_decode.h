@@ -247,10 +247,15 @@ FSK_API int fsk_fp8_decode_table(uint16_t *out, void *stream);
  *   "chunk_tokens"        fixed split size in tokens (0: chosen on the device)
  *   "waves_per_cu"        persistent grid size, workgroups per CU (default 8)
  *   "target_waves_per_cu" automatic split: units of work per CU (default 4)
- * Returns FSK_OK or FSK_ERR_INVALID for an unknown name or bad value. */
+ *   "xcd_skew"            automatic split: extra share of the even XCDs, in %
+ *                         (0..50, default 3; 0 = equal chunks)
+ * The options are process-wide and not synchronised: set them before
+ * decoding from several threads.  Returns FSK_OK or FSK_ERR_INVALID for an
+ * unknown name or bad value. */
 FSK_API int fsk_set_option(const char *name, int64_t value);
 
-/* Profiling hook (no counterpart in the reference; used by the benchmark).
+/* Profiling hook (no counterpart in the reference; used by the benchmark;
+ * process-wide, for one thread at a time).
  * With every_n > 0, every n-th decode or write call launches its kernels with
  * HIP events that the dispatches stamp (hipExtLaunchKernel): for a decode,
  * the split-KV partial kernel's start and end and the reduce kernel's end;
