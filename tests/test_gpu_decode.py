@@ -561,3 +561,30 @@ def test_large_logits_and_sinks(layout, sink_scale):
         ref = oracle_for(wl, mode)
         assert np.isfinite(ref).all()
         run_and_check(wl, sink_mode=mode, what=f"{layout} large logits, sinks x{sink_scale}, {mode}")
+
+
+def test_concurrent_streams_and_threads_match_serial():
+    """Decodes on two streams at once (launched from two host threads, each
+    with its own workspace) give the same bits as the same calls in order."""
+    import threading
+
+    a = W.make("M0", overrides=dict(B=3, lens=("list", [4000, 50, 9000])), seed=31).to(DEV)
+    b = W.make("C1", overrides=dict(B=5, sinks=True), seed=32).to(DEV)
+    want_a, want_b = W.run(a), W.run(b)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    got = {}
+
+    def worker(i, wl):
+        with torch.cuda.stream(streams[i]):
+            outs = [W.run(wl) for _ in range(20)]
+        got[i] = outs
+
+    threads = [threading.Thread(target=worker, args=(0, a)), threading.Thread(target=worker, args=(1, b))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert all(torch.equal(o, want_a) for o in got[0])
+    assert all(torch.equal(o, want_b) for o in got[1])
