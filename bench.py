@@ -360,7 +360,8 @@ def main():
                else None)
 
     out = {
-        "metric": METRIC,
+        "metric": METRIC if args.config == "M0" else (
+            f"µs/step + achieved HBM GB/s (% peak), {base.layout} GQA decode {args.config}"),
         "value": round(gbs, 2),
         "unit": "GB/s",
         "us_per_step": round(ms_step * 1e3, 2),
