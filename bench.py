@@ -52,9 +52,9 @@ def parse():
                     help="replay each decode step from a captured HIP graph (no per-step host work)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--traffic", default=os.path.join(os.path.dirname(os.path.abspath(__file__)),
-                                                      "profiles", "partial_kernel_M0_traffic.md"),
-                    help="rocprof summary holding 'bytes_per_launch: N' for the partial kernel")
+    ap.add_argument("--traffic", default="",
+                    help="rocprof summary holding 'bytes_per_launch: N' for the partial kernel "
+                         "(default: profiles/partial_kernel_<config>_traffic.md, if committed)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration under rocprof)")
     return ap.parse_args()
@@ -356,8 +356,9 @@ def main():
     if args.graph:   # the replay (partial + reduce) is the timed unit
         part_avg_ms = tot_ms / max(calls, 1)
     kern_gbs = alg_bytes / (part_avg_ms / 1e3) / 1e9 if part_avg_ms > 0 else None
-    traffic = (read_traffic(args.traffic) if args.config == "M0" and not (args.chunk or args.graph or args.block_scores)
-               else None)
+    traffic_file = args.traffic or os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                                f"partial_kernel_{args.config}_traffic.md")
+    traffic = None if (args.chunk or args.graph or args.block_scores) else read_traffic(traffic_file)
 
     out = {
         "metric": METRIC if args.config == "M0" else (
