@@ -53,8 +53,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--traffic", default="",
-                    help="rocprof summary holding 'bytes_per_launch: N' for the partial kernel "
-                         "(default: profiles/partial_kernel_<config>_traffic.md, if committed)")
+                    help="rocprof summary holding 'bytes_per_launch: N' for the measured kernel "
+                         "(default: profiles/partial_kernel_<config>_traffic.md, or "
+                         "kv_write_kernel_<config>_traffic.md for W0..W2, if committed)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration under rocprof)")
     return ap.parse_args()
@@ -265,7 +266,8 @@ def bench_write(args):
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(kern_gbs / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": read_traffic(args.traffic or os.path.join(
+                os.path.dirname(os.path.abspath(__file__)), "profiles", f"kv_write_kernel_{args.config}_traffic.md")),
             "kernel": "kv_write_kernel",
             "kernel_avg_us": round(kern_ms * 1e3, 3),
         },
