@@ -240,6 +240,8 @@ def _dense(q, k_cache, v_cache, cache_lens, start_k_offsets, num_splits, *, q_sc
         raise ValueError("cache_lens must have one entry per sequence")
     starts = None if start_k_offsets is None else _int32(start_k_offsets, "start_k_offsets", dev)
     sinks = _sinks(s_aux, Hq, dev)
+    # (the scale tensors stay referenced until the launch: one made here from
+    # a float must not go back to the allocator before the kernel reads it)
     qs, qsp = _scale_ptr(q_scale, dev, "scale_q")
     ks, ksp = _scale_ptr(k_scale, dev, "scale_k")
     vs, vsp = _scale_ptr(v_scale, dev, "scale_v")
@@ -251,10 +253,10 @@ def _dense(q, k_cache, v_cache, cache_lens, start_k_offsets, num_splits, *, q_sc
     nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_DENSE, B, Hq, Hkv, D, S, 16, chunk_tokens, dev.index)
     ws = _workspace(nbytes, dev)
     lib = nat.load()
-    qs, kst, vst, os_ = q.stride(), k.stride(), v.stride(), out.stride()
+    qst, kst, vst, os_ = q.stride(), k.stride(), v.stride(), out.stride()
     st = nat.launch(
         dev.index, lib.fsk_decode_dense,
-        q.data_ptr(), qs[0], qs[1],
+        q.data_ptr(), qst[0], qst[1],
         k.data_ptr(), kst[0], kst[1], kst[2],
         v.data_ptr(), vst[0], vst[1], vst[2], S,
         lens.data_ptr(), nat.ptr(starts), nat.ptr(sinks), _sink_mode(sink_mode), qsp, ksp, vsp,
