@@ -190,6 +190,8 @@ struct Params {
   const float* v_scale;
   float score_scale;       // sm_scale * log2(e)
   int B, Hkv, G, n_hb;
+  int n_items_h;           // head slots per chunk: Hkv * n_hb, or Hkv / 2 with pair
+  int pair;                // varlen, head_dim 64: a wave takes KV heads 2i and 2i+1 as one 128-wide row
   int chunk_min, chunk_max;  // split size bounds in tokens (multiples of 32)
   int target_units;        // preferred number of sequence chunks per call
   int u_max;               // workspace capacity in units
@@ -368,7 +370,7 @@ __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32
   sp.pair = 2 * (int)chunk;
   sp.n = (int)cdiv(total, chunk);
   sp.paired = 0;
-  const int NH = p.Hkv * p.n_hb;
+  const int NH = p.n_items_h;
   if (p.xcd_skew > 0 && chunk >= (uint32_t)kSkewMinChunk && total > 0) {
     // long chunks (1 + skew %) for the even XCDs, short ones for the odd
     // (short splits are latency-bound: there the longer chunks cost more)
@@ -784,8 +786,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
 
   int lane_start, lane_len;  // start and length of sequence `lane` (B <= 64)
   const Split sp = build_plan<kLayout, kScores>(p, s_pre, s_flat, lane_start, lane_len);
-  const int NH = p.Hkv * p.n_hb;
+  const int NH = p.n_items_h;
   const int64_t W = (int64_t)sp.n * NH;
+  // Head pairs (varlen, head_dim 64, instantiated at D = 128): the token rows
+  // of KV heads 2i and 2i+1 are 128-byte neighbours in [T, Hkv, 64], read as
+  // one 256-byte row.  Columns 0..G-1 are head 2i's query heads with Q zero
+  // in dims 64..127, columns G..2G-1 head 2i+1's with Q zero in dims 0..63,
+  // so each column's scores are its own head's; of the 128 output dims a
+  // column keeps its head's half.
+  const bool pair = (kLayout == kVarlen && D == 128 && !kScores) ? (uniform(p.pair) != 0) : false;
   const float k_scale = kKvFp8 ? p.k_scale[0] : 1.0f;
   const float v_scale = kKvFp8 ? p.v_scale[0] : 1.0f;
   const float sscale = p.score_scale * k_scale;
@@ -793,7 +802,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   for (int64_t w = blockIdx.x; w < W; w += gridDim.x) {
     int jc, hh;
     item_of(sp, w, NH, jc, hh);
-    const int kvh = hh / p.n_hb;
+    const int kvh = hh / p.n_hb;  // (with pair: the pair index, n_hb = 1)
     const int hb = hh - kvh * p.n_hb;
     const int lo = chunk_lo(sp, jc), hi = lo + chunk_len(sp, jc);  // stream range of this chunk
     for (int b = uniform(find_seq(s_flat, p.B, lo)); b < p.B; ++b) {
@@ -801,7 +810,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     if (fb >= hi) break;
     Unit un;
     un.b = b;
-    un.kvh = kvh;
+    un.kvh = pair ? 2 * kvh : kvh;
     if (p.B <= kWave) {
       un.start = __builtin_amdgcn_readlane(lane_start, un.b);
       un.len = __builtin_amdgcn_readlane(lane_len, un.b);
@@ -831,15 +840,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     }
 
     // ---- Q^T operand: head c of this head block, zero for padding heads.
-    const int head = hb * 16 + c;
+    // With pair, column c is query head c - G*hs of KV head un.kvh + hs.
+    const int hs = (pair && c >= p.G) ? 1 : 0;
+    const int head = hb * 16 + c - hs * p.G;
     const bool head_ok = head < p.G;
     u32x4 qop[kSteps];
     {
       const uint8_t* qrow =
-          p.q + (int64_t)un.b * p.q_sb + (int64_t)(un.kvh * p.G + (head_ok ? head : 0)) * p.q_sh;
+          p.q + (int64_t)un.b * p.q_sb + (int64_t)((un.kvh + hs) * p.G + (head_ok ? head : 0)) * p.q_sh;
 #pragma unroll
       for (int i = 0; i < kSteps; ++i) {
-        const int d0 = qk_dim0<kKvFp8>(i, g);
+        const int dk = qk_dim0<kKvFp8>(i, g);  // dim of the (paired) K row
+        const int d0 = pair ? (dk & 63) : dk;  // dim of this column's query row
+        const bool q_ok = head_ok && (!pair || (dk >> 6) == hs);
         // Every lane loads (padding heads read head 0's row, then zero it):
         // unconditional loads keep the compiler's wait counts exact.
         u32x4 x;
@@ -857,7 +870,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
         } else {
           x = *(const u32x4*)(qrow + 2 * d0);
         }
-        qop[i] = head_ok ? x : u32x4{0, 0, 0, 0};
+        qop[i] = q_ok ? x : u32x4{0, 0, 0, 0};
       }
     }
     if constexpr (kLayout == kPaged) {
@@ -918,16 +931,22 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     // ---- unit epilogue: fp32 partial for each real head of the block
     const float l_tot = group4_sum(st.l_run);
     if (head_ok) {
-      const int64_t idx = ((int64_t)u * p.Hkv + un.kvh) * p.G + head;
-      float* dst = p.part_acc + idx * D + kDpc * 4 * g;
+      // Lane (g, c) holds dims [kDpc*4*g, kDpc*4*(g+1)) of column c: with
+      // pair (kDpc = 8), k-groups 0-1 hold dims 0..63 and 2-3 dims 64..127,
+      // and a column stores its own head's half into a 64-wide partial.
+      const int64_t idx = ((int64_t)u * p.Hkv + un.kvh + hs) * p.G + head;
+      const int dl = pair ? 64 : D;
+      float* dst = p.part_acc + idx * dl + kDpc * 4 * g - hs * 64;
+      if (!pair || (g >> 1) == hs) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+        for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int j = 0; j < kDpc; j += 4) {
-          const f32x4 o = {st.acc[j][r] * v_scale, st.acc[j + 1][r] * v_scale, st.acc[j + 2][r] * v_scale,
-                           st.acc[j + 3][r] * v_scale};
-          *(f32x4*)(dst + kDpc * r + j) = o;
-        }
+          for (int j = 0; j < kDpc; j += 4) {
+            const f32x4 o = {st.acc[j][r] * v_scale, st.acc[j + 1][r] * v_scale, st.acc[j + 2][r] * v_scale,
+                             st.acc[j + 3][r] * v_scale};
+            *(f32x4*)(dst + kDpc * r + j) = o;
+          }
+      }
       if (g == 0) *(f32x2*)(p.part_ml + 2 * idx) = f32x2{st.m_run, l_tot};
     }
     }  // segments of the chunk
@@ -1426,11 +1445,9 @@ struct SplitPlan {
   int chunk_min, chunk_max, target_units;
   int64_t u_max;
 };
-SplitPlan plan_split(int layout, int B, int Hkv, int n_hb, int64_t kv_extent, int page_size, int chunk_tokens,
-                     int cus) {
+SplitPlan plan_split(int layout, int B, int64_t nh, int64_t kv_extent, int page_size, int chunk_tokens, int cus) {
   SplitPlan sp;
   const int fixed = chunk_tokens > 0 ? chunk_tokens : g_opt.chunk_tokens;
-  const int64_t nh = (int64_t)Hkv * n_hb;
   if (fixed > 0) {
     sp.chunk_min = sp.chunk_max = fixed;
     sp.target_units = 1;
@@ -1445,6 +1462,19 @@ SplitPlan plan_split(int layout, int B, int Hkv, int n_hb, int64_t kv_extent, in
   sp.u_max = std::max(unit_bound(layout, B, kv_extent, page_size, kChunkMax),
                       std::min(unit_bound(layout, B, kv_extent, page_size, kChunkMin), cap));
   return sp;
+}
+
+// Varlen decodes at head_dim 64 with an even number of KV heads and at most
+// 8 query heads per KV head take neighbouring KV heads in pairs (partial_kernel
+// at D = 128) when the heads of a token row are packed; the split is planned
+// for head_dim and head count alone, so the workspace size does not depend on
+// the strides.
+bool pair_shape(int layout, int D, int Hkv, int G) {
+  return layout == FSK_LAYOUT_VARLEN && D == 64 && Hkv % 2 == 0 && G <= 8;
+}
+// Head slots per chunk the split is planned for.
+int64_t plan_heads(int layout, int D, int Hkv, int G) {
+  return pair_shape(layout, D, Hkv, G) ? Hkv / 2 : (int64_t)Hkv * ((G + 15) / 16);
 }
 
 struct WsLayout {
@@ -1607,7 +1637,9 @@ int run_decode(const Common& c) {
   const int n_hb = (G + 15) / 16;
   const int cus = device_cus();
   if (c.chunk < 0 || c.chunk % 32 != 0) return fail(FSK_ERR_INVALID, "chunk_tokens must be 0 or a positive multiple of 32");
-  const SplitPlan sp = plan_split(c.layout, c.B, c.Hkv, n_hb, c.kv_extent, c.page_size, c.chunk, cus);
+  const SplitPlan sp = plan_split(c.layout, c.B, plan_heads(c.layout, c.D, c.Hkv, G), c.kv_extent, c.page_size,
+                                  c.chunk, cus);
+  const bool pair = pair_shape(c.layout, c.D, c.Hkv, G) && !c.scores && c.k_sh == 64 && c.v_sh == 64;
   if (c.layout == FSK_LAYOUT_PAGED && sp.chunk_max > kChunkMax)
     return fail(FSK_ERR_UNSUPPORTED, "paged decode takes chunk_tokens <= 2048");
   const int64_t u_max = sp.u_max;
@@ -1634,6 +1666,8 @@ int run_decode(const Common& c) {
   p.q_scale = c.q_scale; p.k_scale = c.k_scale; p.v_scale = c.v_scale;
   p.score_scale = c.sm_scale * kLog2e;
   p.B = c.B; p.Hkv = c.Hkv; p.G = G; p.n_hb = n_hb;
+  p.pair = pair ? 1 : 0;
+  p.n_items_h = pair ? c.Hkv / 2 : c.Hkv * n_hb;
   p.chunk_min = sp.chunk_min; p.chunk_max = sp.chunk_max; p.target_units = sp.target_units;
   p.xcd_skew = sp.chunk_min == sp.chunk_max ? 0 : g_opt.xcd_skew;  // not with a fixed split
   p.u_max = (int)u_max;
@@ -1659,8 +1693,8 @@ int run_decode(const Common& c) {
   int rc;
   const bool sc = c.scores != nullptr;
   const Launch lp{c.stream, ev[0], ev[1]};
-  if (c.D == 64) rc = dispatch_layout<64>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
-  else if (c.D == 128) rc = dispatch_layout<128>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
+  if (c.D == 64 && !pair) rc = dispatch_layout<64>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
+  else if (c.D <= 128) rc = dispatch_layout<128>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
   else rc = dispatch_layout<256>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
   if (rc != FSK_OK) {
     timing_keep(ev, false);
@@ -1867,9 +1901,9 @@ int64_t fsk_workspace_bytes(int layout, int batch, int num_q_heads, int num_kv_h
   if (layout == FSK_LAYOUT_PAGED && (page_size <= 0 || page_size % 16)) return fail(FSK_ERR_UNSUPPORTED, "page_size must be a positive multiple of 16");
   if (chunk_tokens < 0 || chunk_tokens % 32) return fail(FSK_ERR_INVALID, "chunk_tokens: 0 or a multiple of 32");
   const int G = num_q_heads / num_kv_heads;
-  const int n_hb = (G + 15) / 16;
   const int B = batch > 0 ? batch : 1;
-  const SplitPlan sp = plan_split(layout, B, num_kv_heads, n_hb, kv_extent, page_size, chunk_tokens, device_cus());
+  const SplitPlan sp = plan_split(layout, B, plan_heads(layout, head_dim, num_kv_heads, G), kv_extent, page_size,
+                                  chunk_tokens, device_cus());
   const int64_t u_max = sp.u_max;
   return ws_layout(B, num_kv_heads, G, head_dim, u_max).total;
 }

@@ -260,6 +260,47 @@ def test_varlen_head_dims(D, kv):
     run_and_check(wl, what=f"varlen D={D} {kv}")
 
 
+@pytest.mark.parametrize("Hq,Hkv", [(64, 8), (32, 8), (4, 2), (16, 4)])
+@pytest.mark.parametrize("kv", ["f16", "bf16", "e4m3"])
+@pytest.mark.parametrize("mode", ["exp", "linear"])
+def test_varlen_d64_head_pairs(Hq, Hkv, kv, mode):
+    """Varlen at head_dim 64 reads KV heads 2i and 2i+1 as one 128-wide row
+    when the heads of a token row are packed; the same inputs with the heads
+    spread apart (K/V as views of wider rows) take one head per wave.  Both
+    must match the oracle, over lengths that span many splits, one token and
+    zero tokens, and with sequences crossing split boundaries."""
+    q = "bf16" if kv == "bf16" else "f16"
+    wl = W.make("C1", overrides=dict(B=5, Hq=Hq, Hkv=Hkv, D=64, lens=("list", [6000, 1, 0, 2049, 333]),
+                                      kv=kv, q=q, out=q, sinks=True), seed=41)
+    wl.s_aux = wl.s_aux * 0.1
+    ref = oracle_for(wl, mode)
+    atol, rtol = tol_for(wl)
+    w = wl.to(DEV)
+    out = W.run(w, sink_mode=mode)
+    torch.cuda.synchronize()
+    assert_close(out, ref, atol, rtol, f"paired Hq={Hq} Hkv={Hkv} {kv} {mode}")
+    # heads 256 bytes apart: k[:, h] is no longer next to k[:, h+1]
+    raw = torch.uint8 if kv == "e4m3" else w.k.dtype  # (fp8 moved as bytes)
+    wide_k = torch.zeros(w.k.shape[0], Hkv, 128, dtype=raw, device=DEV)
+    wide_v = torch.zeros_like(wide_k)
+    wide_k[:, :, :64] = w.k.view(raw)
+    wide_v[:, :, :64] = w.v.view(raw)
+    w.k, w.v = wide_k[:, :, :64].view(w.k.dtype), wide_v[:, :, :64].view(w.v.dtype)
+    assert w.k.stride(1) == 128
+    out2 = W.run(w, sink_mode=mode)
+    torch.cuda.synchronize()
+    assert_close(out2, ref, atol, rtol, f"strided heads Hq={Hq} Hkv={Hkv} {kv} {mode}")
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(72, 8), (24, 3)])
+def test_varlen_d64_unpaired_shapes(Hq, Hkv):
+    """head_dim 64 shapes that keep one KV head per wave: more than 8 query
+    heads per KV head, or an odd KV head count."""
+    wl = W.make("C1", overrides=dict(B=3, Hq=Hq, Hkv=Hkv, D=64, lens=("list", [4100, 17, 900]), sinks=True),
+                seed=43)
+    run_and_check(wl, what=f"varlen D=64 Hq={Hq} Hkv={Hkv}")
+
+
 # ---------------------------------------------------------------------------
 # dense (HF cache) and the fp8 reference API
 # ---------------------------------------------------------------------------
