@@ -2,7 +2,8 @@
 //
 // Two kernels per decode call:
 //   1. partial_kernel: a persistent grid of one-wave workgroups walks a device
-//      work list of (sequence chunk, kv head) units.  Each unit streams its
+//      work list of (sequence chunk, kv head) units (varlen at head_dim 64:
+//      a pair of neighbouring kv heads read as one 128-wide row).  Each unit streams its
 //      chunk of K/V in 32-token tiles with 128-bit buffer loads, computes
 //      S^T = K Q^T and O^T += V^T P^T on the matrix cores
 //      (v_mfma_f32_16x16x32_{f16,bf16}), keeps the online-softmax state in the
@@ -10,7 +11,7 @@
 //      query head.  The work list is built by every workgroup from the
 //      sequence lengths (a wave prefix scan into LDS), so the host never reads
 //      lengths back and the grid size only depends on host-known bounds.
-//   2. reduce_kernel: one wave per (sequence, query head) combines the
+//   2. reduce_kernel: one 256-thread workgroup per (sequence, query head) combines the
 //      partials with a log-sum-exp merge, folds the attention sink and writes
 //      the output in the requested dtype.
 //
