@@ -289,14 +289,14 @@ struct Split {
   int n;               // chunks in the call
   int paired;          // items map even chunks to even XCDs (see item_of)
 };
-__device__ __forceinline__ int chunk_of(const Split& sp, int x) {  // x >= 0
+__host__ __device__ __forceinline__ int chunk_of(const Split& sp, int x) {  // x >= 0
   const int q = (int)((uint32_t)x / (uint32_t)sp.pair);
   return 2 * q + (x - q * sp.pair >= sp.c_e ? 1 : 0);
 }
-__device__ __forceinline__ int chunk_lo(const Split& sp, int j) { return (j >> 1) * sp.pair + (j & 1) * sp.c_e; }
+__host__ __device__ __forceinline__ int chunk_lo(const Split& sp, int j) { return (j >> 1) * sp.pair + (j & 1) * sp.c_e; }
 // (arithmetic, not a select: the compiler turns the select into a two-entry
 // table in scratch memory, whose loads are not known to be wave-uniform)
-__device__ __forceinline__ int chunk_len(const Split& sp, int j) { return sp.c_e + (j & 1) * (sp.c_o - sp.c_e); }
+__host__ __device__ __forceinline__ int chunk_len(const Split& sp, int j) { return sp.c_e + (j & 1) * (sp.c_o - sp.c_e); }
 
 // Work item w -> (chunk, head slot).  Workgroups are dealt to the 8 XCDs
 // round-robin (XCD = w mod 8 for the items of the first round), and on this
@@ -305,7 +305,7 @@ __device__ __forceinline__ int chunk_len(const Split& sp, int j) { return sp.c_e
 // takes pair index P = 4 m + x / 2 of its parity class, chunk 2 (P / NH) +
 // (x & 1), head slot P mod NH.  (A bijection when n is even and n NH is a
 // multiple of 8, which the plan ensures before setting `paired`.)
-__device__ __forceinline__ void item_of(const Split& sp, int64_t w, int NH, int& jc, int& hh) {
+__host__ __device__ __forceinline__ void item_of(const Split& sp, int64_t w, int NH, int& jc, int& hh) {
   if (sp.paired) {
     const int x = (int)(w & 7);
     const int64_t P = (w >> 3) * 4 + (x >> 1);
@@ -319,6 +319,60 @@ __device__ __forceinline__ void item_of(const Split& sp, int64_t w, int NH, int&
 }
 
 constexpr int kSkewMinChunk = 512;  // smallest split that gets the XCD skew (tokens)
+
+// The scalar part of the plan: the chunk geometry of a stream of `total`
+// padded tokens (align = the padding, 32 or 128).  Compiled for the host too,
+// so that the split's invariants can be checked without a GPU
+// (fsk_debug_split).
+struct SplitArgs {
+  int chunk_min, chunk_max;  // split size bounds in tokens (multiples of align)
+  int target_units;          // preferred number of chunks
+  int u_max, B;              // workspace capacity in partials, sequences
+  int xcd_skew;              // percent, 0: equal chunks
+  int NH;                    // head slots per chunk (work items = chunks x NH)
+  int align;
+};
+__host__ __device__ __forceinline__ Split split_geometry(uint32_t total, const SplitArgs& a) {
+  auto cdiv = [](uint32_t x, uint32_t y) { return (x + y - 1) / y; };
+  auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
+  auto umin = [](uint32_t x, uint32_t y) { return x < y ? x : y; };
+  const uint32_t align = (uint32_t)a.align;
+  // Chunks per call: target_units, doubled while that would need chunks above
+  // chunk_max (a batch too long for target_units full-size chunks gets twice
+  // as many chunks rather than a count that leaves some CUs one item short).
+  // cdiv(total, t) > chunk_max exactly when t < cdiv(total, chunk_max).
+  const uint32_t chunk_max = (uint32_t)a.chunk_max;
+  const uint32_t t_need = cdiv(total, chunk_max);
+  uint32_t target = (uint32_t)a.target_units;
+  while (target < t_need && target < (1u << 24)) target *= 2;
+  uint32_t want = cdiv(total, target);
+  const uint32_t cap = a.u_max > a.B + 1 ? (uint32_t)(a.u_max - a.B - 1) : 0;  // chunks the workspace holds
+  want = cap > 0 ? umax(want, cdiv(total, cap)) : chunk_max;
+  want = (want + align - 1) / align * align;
+  const uint32_t chunk = umin(umax(want, (uint32_t)a.chunk_min), chunk_max);
+  Split sp;
+  sp.c_e = sp.c_o = (int)chunk;
+  sp.n = (int)cdiv(total, chunk);
+  sp.paired = 0;
+  if (a.xcd_skew > 0 && chunk >= (uint32_t)kSkewMinChunk && total > 0) {
+    // long chunks (1 + skew %) for the even XCDs, short ones for the odd
+    // (short splits are latency-bound: there the longer chunks cost more)
+    uint32_t ce = (chunk * (uint32_t)(100 + a.xcd_skew) / 100 + align - 1) / align * align;
+    ce = umin(ce, chunk_max);
+    const uint32_t co = 2 * chunk - ce;
+    const uint32_t q = total / (2 * chunk), r = total - q * 2 * chunk;
+    uint32_t n = 2 * q + (r > 0 ? 1 : 0) + (r > ce ? 1 : 0);
+    n += n & 1;  // even: a trailing chunk past the stream has no tokens
+    if (co >= align && co < ce && n <= cap && ((int64_t)n * a.NH) % 8 == 0) {
+      sp.c_e = (int)ce;
+      sp.c_o = (int)co;
+      sp.n = (int)n;
+      sp.paired = 1;
+    }
+  }
+  sp.pair = sp.c_e + sp.c_o;
+  return sp;
+}
 
 template <int kLayout, bool kScores>
 __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32_t* flat, int& start0_out,
@@ -352,42 +406,8 @@ __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32
     total += (uint32_t)__builtin_amdgcn_readlane(wave_incl_sum(padded), kWave - 1);
   }
   total = (uint32_t)uniform((int)total);
-  auto cdiv = [](uint32_t a, uint32_t b) { return (a + b - 1) / b; };
-  // Chunks per call: target_units, doubled while that would need chunks above
-  // chunk_max (a batch too long for target_units full-size chunks gets twice
-  // as many chunks rather than a count that leaves some CUs one item short).
-  // cdiv(total, t) > chunk_max exactly when t < cdiv(total, chunk_max).
-  const uint32_t chunk_max = (uint32_t)p.chunk_max;
-  const uint32_t t_need = cdiv(total, chunk_max);
-  uint32_t target = (uint32_t)p.target_units;
-  while (target < t_need && target < (1u << 24)) target *= 2;
-  uint32_t want = cdiv(total, target);
-  const uint32_t cap = p.u_max > p.B + 1 ? (uint32_t)(p.u_max - p.B - 1) : 0;  // chunks the workspace holds
-  want = cap > 0 ? max(want, cdiv(total, cap)) : chunk_max;
-  want = (want + kAlign - 1) / kAlign * kAlign;
-  const uint32_t chunk = (uint32_t)uniform((int)min(max(want, (uint32_t)p.chunk_min), chunk_max));
-  Split sp;
-  sp.c_e = sp.c_o = (int)chunk;
-  sp.pair = 2 * (int)chunk;
-  sp.n = (int)cdiv(total, chunk);
-  sp.paired = 0;
-  const int NH = p.n_items_h;
-  if (p.xcd_skew > 0 && chunk >= (uint32_t)kSkewMinChunk && total > 0) {
-    // long chunks (1 + skew %) for the even XCDs, short ones for the odd
-    // (short splits are latency-bound: there the longer chunks cost more)
-    uint32_t ce = (chunk * (uint32_t)(100 + p.xcd_skew) / 100 + kAlign - 1) / kAlign * kAlign;
-    ce = min(ce, chunk_max);
-    const uint32_t co = 2 * chunk - ce;
-    const uint32_t q = total / (2 * chunk), r = total - q * 2 * chunk;
-    uint32_t n = 2 * q + (r > 0 ? 1 : 0) + (r > ce ? 1 : 0);
-    n += n & 1;  // even: a trailing chunk past the stream has no tokens
-    if (co >= (uint32_t)kAlign && co < ce && n <= cap && ((int64_t)n * NH) % 8 == 0) {
-      sp.c_e = (int)ce;
-      sp.c_o = (int)co;
-      sp.n = (int)n;
-      sp.paired = 1;
-    }
-  }
+  const SplitArgs sa{p.chunk_min, p.chunk_max, p.target_units, p.u_max, p.B, p.xcd_skew, p.n_items_h, kAlign};
+  Split sp = split_geometry(total, sa);
   sp.c_e = uniform(sp.c_e);
   sp.c_o = uniform(sp.c_o);
   sp.pair = sp.c_e + sp.c_o;
@@ -2089,6 +2109,40 @@ int fsk_fp8_decode_table(uint16_t* out, void* stream) {
   hipLaunchKernelGGL(fp8_table_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, (uint32_t*)out);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(FSK_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
+  return FSK_OK;
+}
+
+int fsk_debug_split(int64_t total, int chunk_min, int chunk_max, int target_units, int64_t u_max, int batch,
+                    int xcd_skew, int head_slots, int align, int32_t* geometry, int32_t* chunk_start,
+                    int32_t* item_chunk, int32_t* item_slot, int32_t* token_chunk) {
+  if (!geometry) return fail(FSK_ERR_INVALID, "null geometry");
+  if (total < 0 || total >= ((int64_t)1 << 31) - 4096) return fail(FSK_ERR_INVALID, "total out of range");
+  if (align != 32 && align != 128) return fail(FSK_ERR_INVALID, "align must be 32 or 128");
+  if (chunk_min < 32 || chunk_min % align || chunk_max < chunk_min || chunk_max % align || chunk_max > (1 << 24))
+    return fail(FSK_ERR_INVALID, "chunk bounds must be multiples of align with 32 <= chunk_min <= chunk_max");
+  if (target_units < 1 || u_max < 0 || u_max >= ((int64_t)1 << 31) || batch < 0 || xcd_skew < 0 || xcd_skew > 50 ||
+      head_slots < 1 || head_slots > (1 << 16))
+    return fail(FSK_ERR_INVALID, "bad split arguments");
+  const SplitArgs a{chunk_min, chunk_max, target_units, (int)u_max, batch, xcd_skew, head_slots, align};
+  const Split sp = split_geometry((uint32_t)total, a);
+  geometry[0] = sp.c_e;
+  geometry[1] = sp.c_o;
+  geometry[2] = sp.n;
+  geometry[3] = sp.paired;
+  if (chunk_start)
+    for (int j = 0; j < sp.n; ++j) chunk_start[j] = chunk_lo(sp, j);
+  if (item_chunk && item_slot) {
+    const int64_t W = (int64_t)sp.n * head_slots;
+    if (W >= ((int64_t)1 << 31)) return fail(FSK_ERR_UNSUPPORTED, "too many work items");
+    for (int64_t w = 0; w < W; ++w) {
+      int jc, hh;
+      item_of(sp, w, head_slots, jc, hh);
+      item_chunk[w] = jc;
+      item_slot[w] = hh;
+    }
+  }
+  if (token_chunk)
+    for (int64_t x = 0; x < total; ++x) token_chunk[x] = chunk_of(sp, (int)x);
   return FSK_OK;
 }
 

@@ -243,6 +243,25 @@ FSK_API int fsk_paged_gather(const void *pool, int64_t stride_p, int64_t stride_
  * :90-92). */
 FSK_API int fsk_fp8_decode_table(uint16_t *out, void *stream);
 
+/* Debug: the chunk geometry and work-item mapping of the decode kernels'
+ * device-side plan, computed on the host by the same functions, for a stream
+ * of `total` padded tokens (each sequence padded to `align` = 32, or 128 with
+ * block scores).  chunk_min / chunk_max / target_units / u_max / xcd_skew are
+ * the split policy a decode call passes to its kernel; head_slots = work items
+ * per chunk.  geometry[0..3] = long chunk, short chunk (equal without an XCD
+ * skew), chunk count n, XCD pairing flag.  Optional outputs (null to skip):
+ * chunk_start[n]; item_chunk[n * head_slots] and item_slot[...] (the chunk
+ * and head slot of work item w); token_chunk[total] (the chunk holding
+ * stream position x).  No GPU needed.  The split follows the reference's
+ * split-KV partition (fskernels/triton/triton_gqa_decode_hf.py:52-54), with
+ * the chunk count chosen for this GPU. */
+FSK_API int fsk_debug_split(int64_t total, int chunk_min, int chunk_max,
+                            int target_units, int64_t u_max, int batch,
+                            int xcd_skew, int head_slots, int align,
+                            int32_t *geometry, int32_t *chunk_start,
+                            int32_t *item_chunk, int32_t *item_slot,
+                            int32_t *token_chunk);
+
 /* Tuning knobs for benchmarking sweeps:
  *   "chunk_tokens"        fixed split size in tokens (0: chosen on the device)
  *   "waves_per_cu"        persistent grid size, workgroups per CU (default 8)

@@ -1,0 +1,141 @@
+"""Invariants of the decode kernels' device-side work plan, checked on the host.
+
+fsk_debug_split runs the same split_geometry / chunk_lo / chunk_of / item_of
+code that every workgroup of the partial kernel runs, compiled for the host.
+The split policy arguments are the ones a decode call passes (automatic
+splits: chunk bounds 128..2048 tokens, 4 items per CU, the workspace capacity
+the host sizes; fixed splits: one chunk size, no XCD skew).  Checked: chunk
+sizes and alignment, contiguous coverage of the token stream, the token ->
+chunk map, room for every partial in the workspace, and that work items map
+one-to-one onto (chunk, head slot) pairs with the long chunks on even XCDs.
+No GPU needed.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from fasterkernels_amd import _native as nat
+
+CHUNK_MIN, CHUNK_MAX, SKEW_MIN = 128, 2048, 512
+
+
+def cdiv(a, b):
+    return -(-a // b)
+
+
+def host_policy(total, B, NH, cus, fixed=0, skew=3):
+    """(chunk_min, chunk_max, target_units, u_max, xcd_skew) as the host sets
+    them for a stream of `total` padded tokens (stream bound total + 128 B)."""
+    bound = total + 128 * B
+
+    def unit_bound(c):
+        return cdiv(bound, c) + B + 1
+
+    if fixed:
+        return fixed, fixed, 1, unit_bound(fixed), 0
+    target = max(1, cus * 4 // NH)
+    cap = max(4 * target, 256)
+    return CHUNK_MIN, CHUNK_MAX, target, max(unit_bound(CHUNK_MAX), min(unit_bound(CHUNK_MIN), cap)), skew
+
+
+def split(total, cmin, cmax, target, u_max, B, skew, NH, align):
+    lib = nat.load()
+    geo = (ctypes.c_int32 * 4)()
+    nat.check(lib.fsk_debug_split(total, cmin, cmax, target, u_max, B, skew, NH, align, geo, None, None, None, None))
+    ce, co, n, paired = list(geo)
+    starts = np.zeros(max(n, 1), np.int32)
+    ic = np.zeros(max(n * NH, 1), np.int32)
+    isl = np.zeros(max(n * NH, 1), np.int32)
+    tok = np.zeros(max(total, 1), np.int32)
+    nat.check(lib.fsk_debug_split(total, cmin, cmax, target, u_max, B, skew, NH, align, geo,
+                                  starts.ctypes.data, ic.ctypes.data, isl.ctypes.data, tok.ctypes.data))
+    return ce, co, n, bool(paired), starts[:n], ic[:n * NH], isl[:n * NH], tok[:total]
+
+
+def check_case(total, B, NH, cus, fixed, skew, align):
+    cmin, cmax, target, u_max, skew = host_policy(total, B, NH, cus, fixed, skew)
+    ce, co, n, paired, starts, ic, isl, tok = split(total, cmin, cmax, target, u_max, B, skew, NH, align)
+    what = f"total={total} B={B} NH={NH} cus={cus} fixed={fixed} skew={skew} align={align}: ce={ce} co={co} n={n}"
+    # chunk sizes
+    assert ce % align == 0 and co % align == 0 and co >= align and ce <= cmax, what
+    if paired:
+        assert skew > 0 and co < ce and (ce + co) % 2 == 0 and (ce + co) // 2 >= SKEW_MIN, what
+        assert n % 2 == 0 and (n * NH) % 8 == 0, what
+    else:
+        assert ce == co and cmin <= ce <= cmax, what
+    # contiguous coverage of [0, total): chunk j starts where chunk j-1 ends
+    lens = np.where(np.arange(n) % 2 == 0, ce, co)
+    assert n == len(starts)
+    if n:
+        assert starts[0] == 0, what
+        assert np.array_equal(starts[1:], np.cumsum(lens)[:-1]), what
+    if total == 0:
+        assert n == 0, what
+    else:
+        assert starts[-1] + lens[-1] >= total, what
+        # at most the one trailing chunk an even count adds lies past the stream
+        assert starts[-1] < total or (paired and starts[-2] < total), what
+    # token -> chunk map
+    x = np.arange(total)
+    assert np.array_equal(tok, np.searchsorted(starts, x, side="right") - 1), what
+    # every partial fits: at most n + B of them, and the workspace holds u_max
+    assert n + B + 1 <= u_max, what
+    # work items: a bijection onto (chunk, head slot), long chunks on even XCDs
+    assert ((ic >= 0) & (ic < n) & (isl >= 0) & (isl < NH)).all(), what
+    assert len(np.unique(ic.astype(np.int64) * NH + isl)) == n * NH, what
+    if paired:
+        assert np.array_equal(ic % 2, np.arange(n * NH) % 2), what
+    return paired
+
+
+def test_split_rejects_bad_arguments():
+    lib = nat.load()
+    geo = (ctypes.c_int32 * 4)()
+    bad = [
+        (-1, 128, 2048, 1, 100, 1, 0, 8, 32),
+        (100, 16, 2048, 1, 100, 1, 0, 8, 32),      # chunk_min below 32
+        (100, 128, 64, 1, 100, 1, 0, 8, 32),       # chunk_max below chunk_min
+        (100, 96, 2048, 1, 100, 1, 0, 8, 128),     # not a multiple of align
+        (100, 128, 2048, 0, 100, 1, 0, 8, 32),     # no target
+        (100, 128, 2048, 1, 100, 1, 0, 0, 32),     # no head slots
+        (100, 128, 2048, 1, 100, 1, 0, 8, 48),     # align
+        (100, 128, 2048, 1, 100, 1, 51, 8, 32),    # skew
+    ]
+    for args in bad:
+        assert lib.fsk_debug_split(*args, geo, None, None, None, None) == nat.FSK_ERR_INVALID, args
+
+
+@pytest.mark.parametrize("total", [0, 32, 128, 4096, 131072, 131072 + 32, 1_000_000])
+@pytest.mark.parametrize("NH", [8, 4, 16, 3])
+def test_split_headline_and_edge_streams(total, NH):
+    for align in (32, 128):
+        total_a = cdiv(total, align) * align
+        check_case(total_a, 4, NH, 256, 0, 3, align)
+
+
+def test_split_m0_geometry():
+    """M0: 131072 tokens, 8 KV heads, 256 CUs -> 1056/992-token chunk pairs,
+    128 chunks, the long ones on the even XCDs."""
+    ce, co, n, paired, *_ = split(131072, *host_policy(131072, 4, 8, 256)[:4], 4, 3, 8, 32)
+    assert (ce, co, n, paired) == (1056, 992, 128, True)
+
+
+def test_split_random_policies():
+    r = np.random.default_rng(0)
+    seen_paired = seen_plain = 0
+    for _ in range(1500):
+        align = int(r.choice([32, 128]))
+        B = int(r.integers(1, 300))
+        total = int(r.choice([r.integers(0, 5000), r.integers(0, 300_000), r.integers(0, 3_000_000)]))
+        total = cdiv(total, align) * align
+        NH = int(r.choice([1, 2, 3, 4, 5, 8, 12, 16, 32, 64]))
+        cus = int(r.choice([1, 32, 80, 256, 304]))
+        fixed = int(r.choice([0, 0, 0, align, 2 * align, 1024, 4096])) if align == 32 else int(
+            r.choice([0, 0, 0, 128, 256, 2048]))
+        skew = int(r.choice([0, 3, 6, 20, 50]))
+        if check_case(total, B, NH, cus, fixed, skew, align):
+            seen_paired += 1
+        else:
+            seen_plain += 1
+    assert seen_paired > 100 and seen_plain > 100
