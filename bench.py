@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--chunk", type=int, default=0, help="split size in tokens (0: library default)")
     ap.add_argument("--block-scores", action="store_true",
                     help="also compute the pooled 128-token block scores in each step")
+    ap.add_argument("--qk-engine", choices=["mfma", "valu"], default="mfma",
+                    help="QK/PV on the matrix cores (default) or the VALU tile (A/B measurement; f16, D=128)")
     ap.add_argument("--graph", action="store_true",
                     help="replay each decode step from a captured HIP graph (no per-step host work)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
@@ -298,6 +300,7 @@ def main():
         return
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    nat.set_option("qk_engine", 1 if args.qk_engine == "valu" else 0)
     base = W.make(args.config, gen_device=dev, device=dev)
     kv_bytes = base.k.numel() * base.k.element_size() * 2
     n_sets = args.sets or rotation_sets(kv_bytes)
@@ -360,7 +363,8 @@ def main():
     kern_gbs = alg_bytes / (part_avg_ms / 1e3) / 1e9 if part_avg_ms > 0 else None
     traffic_file = args.traffic or os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                                 f"partial_kernel_{args.config}_traffic.md")
-    traffic = None if (args.chunk or args.graph or args.block_scores) else read_traffic(traffic_file)
+    traffic = (None if (args.chunk or args.graph or args.block_scores or args.qk_engine != "mfma")
+               else read_traffic(traffic_file))
 
     out = {
         "metric": METRIC if args.config == "M0" else (
@@ -384,6 +388,7 @@ def main():
             "batch": base.B, "total_tokens": base.total_tokens, "algorithmic_bytes": alg_bytes,
             "chunk_tokens": args.chunk or "auto",
             "launch": "hip graph replay" if args.graph else "eager",
+            "qk_engine": args.qk_engine,
             "block_scores": bool(args.block_scores),
         },
         "roofline": {

@@ -777,13 +777,115 @@ struct BlockMax {
   }
 };
 
+// ---------------------------------------------------------------------------
+// VALU formulation of a tile: the counterpart of compute_tile without matrix
+// cores, kept for A/B measurement (option qk_engine = 1; f16 Q and KV,
+// D = 128, at most 4 query heads per KV head, no block scores).  Lane (g, c)
+// owns dims [8c, 8c+8) of tokens 4g+r and 16+4g+r (r = 0..3) of the tile:
+// the rows and dims its V registers already hold.  Scores: partial q.k over
+// its 8 dims with v_dot2_f32_f16, summed over the 16 lanes of its DPP row;
+// then the online softmax of each head (the 4 k-groups combined with the
+// permlane swaps) and P.V as fp32 FMAs into the lane's 8 dims of each head,
+// with P rounded to f16 first as the MFMA path does.  The k-groups' output
+// sums are combined once per unit.
+// ---------------------------------------------------------------------------
+constexpr int kValuHeads = 4;
+struct SoftmaxV {
+  float m_run[kValuHeads], l_run[kValuHeads];
+  float acc[kValuHeads][8];
+};
+
+// Sum over the 16 lanes of a DPP row (every lane gets it): quad_perm
+// [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += u2f(__builtin_amdgcn_update_dpp(0, f2u(x), 0xB1, 0xf, 0xf, false));
+  x += u2f(__builtin_amdgcn_update_dpp(0, f2u(x), 0x4E, 0xf, 0xf, false));
+  x += u2f(__builtin_amdgcn_update_dpp(0, f2u(x), 0x141, 0xf, 0xf, false));
+  x += u2f(__builtin_amdgcn_update_dpp(0, f2u(x), 0x140, 0xf, 0xf, false));
+  return x;
+}
+
+__device__ __forceinline__ f16x2 as_f16x2(uint32_t w) { return __builtin_bit_cast(f16x2, w); }
+
+template <int D>
+__device__ __forceinline__ void compute_tile_valu(const TileRegs<D, kF16>& T, uint32_t kstage, SoftmaxV& st,
+                                                  const u32x4 (&qv)[kValuHeads], float sscale, int g, int c) {
+  static_assert(D == 128, "the VALU tile covers D = 128 (16 lanes x 8 dims)");
+  // ---- S = q.k: 8 token slots (i = 4 h2 + r) x 4 heads per lane
+  float s[8][kValuHeads];
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const u32x4 kk = k_chunk<D, kF16>(kstage, h2, 4 * g + r, c);
+      uint32_t kw[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) kw[e] = kk[e];
+#pragma unroll
+      for (int h = 0; h < kValuHeads; ++h) {
+        float a = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t qw = qv[h][e];
+          a = __builtin_amdgcn_fdot2(as_f16x2(kw[e]), as_f16x2(qw), a, false);
+        }
+        s[4 * h2 + r][h] = a;
+      }
+    }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int h = 0; h < kValuHeads; ++h) s[i][h] = row16_sum(s[i][h]);
+
+  // ---- V rows of the lane's slots, widened once
+  float vf[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t w = T.v[i].w[e];
+      const f16x2 h = as_f16x2(w);
+      vf[i][2 * e] = (float)h[0];
+      vf[i][2 * e + 1] = (float)h[1];
+    }
+
+  // ---- online softmax and P.V, head by head (log2 domain)
+#pragma unroll
+  for (int h = 0; h < kValuHeads; ++h) {
+    float mt = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float x = s[i][h] * sscale;
+      if (4 * g + (i & 3) >= T.nrow[i >> 2]) x = -INFINITY;
+      s[i][h] = x;
+      mt = fmaxf(mt, x);
+    }
+    mt = group4_max(mt);
+    const float m_new = fmaxf(st.m_run[h], mt);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(st.m_run[h] - m_use);
+    st.m_run[h] = m_new;
+    st.l_run[h] *= alpha;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) st.acc[h][d] *= alpha;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float pv = __builtin_amdgcn_exp2f(s[i][h] - m_use);
+      st.l_run[h] += pv;
+      const float pr = (float)(f16)pv;  // P in the PV operand type
+#pragma unroll
+      for (int d = 0; d < 8; ++d) st.acc[h][d] = fmaf(pr, vf[i][d], st.acc[h][d]);
+    }
+  }
+}
+
 #ifndef FSK_PIPE_DEPTH
 #define FSK_PIPE_DEPTH 2
 #endif
 // Waves per SIMD the register budget is sized for (2: <= 256 VGPRs).
 constexpr int kWavesPerEu = FSK_PIPE_DEPTH > 2 ? 1 : 2;
 
-template <int D, int kQ, int kKV, int kLayout, bool kScores>
+template <int D, int kQ, int kKV, int kLayout, bool kScores, bool kValu = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu))) void partial_kernel(Params p) {
   using TR = TileRegs<D, kKV>;
   using SM = Softmax<D, kQ, kKV>;
@@ -794,6 +896,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   constexpr int kDepth = (D <= 128) ? FSK_PIPE_DEPTH : 1;
   static_assert(kKV != kBF16 || kQ == kBF16, "bf16 KV needs bf16 Q");
   static_assert(kKV != kF16 || kQ != kBF16, "f16 KV needs f16 Q");
+  static_assert(!kValu || (D == 128 && kQ == kF16 && kKV == kF16 && !kScores && kLayout != kDense),
+                "the VALU tile is built for f16, D = 128, paged and varlen");
 
   __shared__ __attribute__((aligned(16))) uint8_t s_kstage_mem[kDepth * 2 * TR::kHalfBytes];
   // LDS offset of the stage = low 32 bits of its generic address
@@ -815,7 +919,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   // in dims 64..127, columns G..2G-1 head 2i+1's with Q zero in dims 0..63,
   // so each column's scores are its own head's; of the 128 output dims a
   // column keeps its head's half.
-  const bool pair = (kLayout == kVarlen && D == 128 && !kScores) ? (uniform(p.pair) != 0) : false;
+  const bool pair = (kLayout == kVarlen && D == 128 && !kScores && !kValu) ? (uniform(p.pair) != 0) : false;
   const float k_scale = kKvFp8 ? p.k_scale[0] : 1.0f;
   const float v_scale = kKvFp8 ? p.v_scale[0] : 1.0f;
   const float sscale = p.score_scale * k_scale;
@@ -894,6 +998,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
         qop[i] = q_ok ? x : u32x4{0, 0, 0, 0};
       }
     }
+    // VALU tile: dims [8c, 8c+8) of each of the (up to 4) query heads
+    u32x4 qv[kValuHeads];
+    if constexpr (kValu) {
+#pragma unroll
+      for (int h = 0; h < kValuHeads; ++h) {
+        const uint8_t* qr = p.q + (int64_t)un.b * p.q_sb + (int64_t)(un.kvh * p.G + min(h, p.G - 1)) * p.q_sh;
+        const u32x4 x = *(const u32x4*)(qr + 16 * c);
+        qv[h] = h < p.G ? x : u32x4{0, 0, 0, 0};
+      }
+    }
     if constexpr (kLayout == kPaged) {
       un.win0 = clampi(win_raw0, 0, p.num_pages - 1);
       un.win1 = clampi(win_raw1, 0, p.num_pages - 1);
@@ -904,6 +1018,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     st.l_run = 0.f;
 #pragma unroll
     for (int j = 0; j < kDpc; ++j) st.acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    SoftmaxV sv;
+    if constexpr (kValu) {
+#pragma unroll
+      for (int h = 0; h < kValuHeads; ++h) {
+        sv.m_run[h] = -INFINITY;
+        sv.l_run[h] = 0.f;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) sv.acc[h][d] = 0.f;
+      }
+    }
     BlockMax bm;
 
     if constexpr (kDepth > 1) {
@@ -931,9 +1055,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
             const int sn = (s + kDepth - 1) % kDepth;
             issue_tile<D, kKV, kLayout>(tiles[sn], s_kstage + sn * 2 * TR::kHalfBytes, p, un, tn, g, c);
             wait_k_stage<TR::kLoads, kDepth>(kDepth - 1);
-            const float mt = compute_tile<D, kQ, kKV>(tiles[s], s_kstage + s * 2 * TR::kHalfBytes, st, qop,
-                                                      sscale, g, c);
-            if constexpr (kScores) bm.add(p, un, un.t_begin + 32 * k, mt, head, head_ok, g);
+            if constexpr (kValu) {
+              compute_tile_valu<D>(tiles[s], s_kstage + s * 2 * TR::kHalfBytes, sv, qv, sscale, g, c);
+            } else {
+              const float mt = compute_tile<D, kQ, kKV>(tiles[s], s_kstage + s * 2 * TR::kHalfBytes, st, qop,
+                                                        sscale, g, c);
+              if constexpr (kScores) bm.add(p, un, un.t_begin + 32 * k, mt, head, head_ok, g);
+            }
             ++k;
             done = k >= n_tiles;
           }
@@ -944,12 +1072,35 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
       for (int t = un.t_begin; t < un.t_end; t += 32) {
         issue_tile<D, kKV, kLayout>(ta, s_kstage, p, un, t, g, c);
         wait_k_stage<TR::kLoads, 1>(0);
-        const float mt = compute_tile<D, kQ, kKV>(ta, s_kstage, st, qop, sscale, g, c);
-        if constexpr (kScores) bm.add(p, un, t, mt, head, head_ok, g);
+        if constexpr (kValu) {
+          compute_tile_valu<D>(ta, s_kstage, sv, qv, sscale, g, c);
+        } else {
+          const float mt = compute_tile<D, kQ, kKV>(ta, s_kstage, st, qop, sscale, g, c);
+          if constexpr (kScores) bm.add(p, un, t, mt, head, head_ok, g);
+        }
       }
     }
 
     // ---- unit epilogue: fp32 partial for each real head of the block
+    if constexpr (kValu) {
+      // k-group g holds the sums over its tokens: combine the four, then the
+      // lanes of k-group 0 store dims [8c, 8c+8) of every head.
+#pragma unroll
+      for (int h = 0; h < kValuHeads; ++h) {
+        const float l_h = group4_sum(sv.l_run[h]);
+        float o[8];
+#pragma unroll
+        for (int d = 0; d < 8; ++d) o[d] = group4_sum(sv.acc[h][d]);
+        if (h < p.G && g == 0) {
+          const int64_t idx = ((int64_t)u * p.Hkv + un.kvh) * p.G + h;
+          float* dst = p.part_acc + idx * D + 8 * c;
+          *(f32x4*)dst = f32x4{o[0], o[1], o[2], o[3]};
+          *(f32x4*)(dst + 4) = f32x4{o[4], o[5], o[6], o[7]};
+          if (c == 0) *(f32x2*)(p.part_ml + 2 * idx) = f32x2{sv.m_run[h], l_h};
+        }
+      }
+      continue;
+    }
     const float l_tot = group4_sum(st.l_run);
     if (head_ok) {
       // Lane (g, c) holds dims [kDpc*4*g, kDpc*4*(g+1)) of column c: with
@@ -1365,6 +1516,7 @@ struct Options {
   int waves_per_cu = 8;         // persistent grid size (workgroups per CU)
   int target_waves_per_cu = 4;  // automatic split: units of work per CU
   int xcd_skew = 3;             // automatic split: extra share of the even XCDs, in % (see item_of)
+  int qk_engine = 0;            // 0: QK and PV on the matrix cores; 1: the VALU tile (A/B measurement)
 } g_opt;
 
 // Event triples of timed decode calls (the partial kernel's start and end and
@@ -1630,6 +1782,15 @@ int dispatch_qkv(const Params& p, int grid, int q_dt, int kv_dt, const Launch& s
   return FSK_OK;
 }
 
+// The VALU-tile kernels (option qk_engine = 1; f16, D = 128, paged or varlen).
+int launch_valu(int layout, const Params& p, int grid, const Launch& s) {
+  if (layout == FSK_LAYOUT_PAGED)
+    launch(partial_kernel<128, kF16, kF16, kPaged, false, true>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p);
+  else
+    launch(partial_kernel<128, kF16, kF16, kVarlen, false, true>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p);
+  return FSK_OK;
+}
+
 template <int D>
 int dispatch_layout(int layout, bool scores, const Params& p, int grid, int q_dt, int kv_dt, const Launch& s) {
   if (layout == FSK_LAYOUT_VARLEN)
@@ -1702,6 +1863,12 @@ int run_decode(const Common& c) {
     p.lens_out = (int32_t*)(ws + wl.total + align256((int64_t)c.B * c.Hq * c.nblk * 4));
   }
 
+  const bool valu = g_opt.qk_engine == 1;
+  if (valu && !(c.D == 128 && c.q_dt == FSK_F16 && c.kv_dt == FSK_F16 && G <= kValuHeads && !c.scores &&
+                c.layout != FSK_LAYOUT_DENSE))
+    return fail(FSK_ERR_UNSUPPORTED, "qk_engine 1 (VALU tile) covers f16 q and KV, head_dim 128, at most 4 query "
+                                     "heads per KV head, the paged and varlen layouts and no block scores");
+
   const int64_t w_max = u_max * c.Hkv * n_hb;
   const int64_t grid64 = std::min<int64_t>(w_max, (int64_t)cus * g_opt.waves_per_cu);
   const int grid = (int)std::max<int64_t>(grid64, 1);
@@ -1714,7 +1881,8 @@ int run_decode(const Common& c) {
   int rc;
   const bool sc = c.scores != nullptr;
   const Launch lp{c.stream, ev[0], ev[1]};
-  if (c.D == 64 && !pair) rc = dispatch_layout<64>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
+  if (valu) rc = launch_valu(c.layout, p, grid, lp);
+  else if (c.D == 64 && !pair) rc = dispatch_layout<64>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
   else if (c.D <= 128) rc = dispatch_layout<128>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
   else rc = dispatch_layout<256>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
   if (rc != FSK_OK) {
@@ -1860,6 +2028,11 @@ int fsk_set_option(const char* name, int64_t value) {
   if (!strcmp(name, "waves_per_cu")) {
     if (value < 1 || value > 64) return fail(FSK_ERR_INVALID, "waves_per_cu in [1, 64]");
     g_opt.waves_per_cu = (int)value;
+    return FSK_OK;
+  }
+  if (!strcmp(name, "qk_engine")) {
+    if (value != 0 && value != 1) return fail(FSK_ERR_INVALID, "qk_engine is 0 (MFMA) or 1 (VALU)");
+    g_opt.qk_engine = (int)value;
     return FSK_OK;
   }
   if (!strcmp(name, "xcd_skew")) {

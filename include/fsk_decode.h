@@ -268,6 +268,12 @@ FSK_API int fsk_debug_split(int64_t total, int chunk_min, int chunk_max,
  *   "target_waves_per_cu" automatic split: units of work per CU (default 4)
  *   "xcd_skew"            automatic split: extra share of the even XCDs, in %
  *                         (0..50, default 3; 0 = equal chunks)
+ *   "qk_engine"           0 (default): QK and PV on the matrix cores (MFMA);
+ *                         1: the VALU formulation of the tile, for A/B
+ *                         measurement (f16 q and KV, head_dim 128, at most 4
+ *                         query heads per KV head, paged and varlen layouts,
+ *                         no block scores; other calls return
+ *                         FSK_ERR_UNSUPPORTED)
  * The options are process-wide and not synchronised: set them before
  * decoding from several threads.  Returns FSK_OK or FSK_ERR_INVALID for an
  * unknown name or bad value. */

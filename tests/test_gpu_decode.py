@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 import torch
 
+from fasterkernels_amd import _native as nat
 from fasterkernels_amd import workloads as W
 from fasterkernels_amd.hip import decode as dec
 from oracle import decode_oracle as O
@@ -299,6 +300,38 @@ def test_varlen_d64_unpaired_shapes(Hq, Hkv):
     wl = W.make("C1", overrides=dict(B=3, Hq=Hq, Hkv=Hkv, D=64, lens=("list", [4100, 17, 900]), sinks=True),
                 seed=43)
     run_and_check(wl, what=f"varlen D=64 Hq={Hq} Hkv={Hkv}")
+
+
+@pytest.fixture
+def valu_engine():
+    nat.set_option("qk_engine", 1)
+    try:
+        yield
+    finally:
+        nat.set_option("qk_engine", 0)
+
+
+@pytest.mark.parametrize("name,ov", [
+    ("M0", dict(B=3, lens=("list", [1, 700, 3000]))),
+    ("M0", dict(B=2, Hq=8, Hkv=8, lens=("list", [5000, 17]), sinks=True)),      # one query head per KV head
+    ("C1", dict(B=4, lens=("list", [0, 33, 2049, 5000]), sinks=True)),
+    ("C1", dict(B=3, Hq=16, Hkv=8, lens=("list", [1, 4100, 640]), sinks=True)),  # two per KV head
+])
+@pytest.mark.parametrize("mode", ["exp", "linear"])
+def test_valu_tile_matches_oracle(valu_engine, name, ov, mode):
+    """The VALU formulation of the tile (option qk_engine = 1, kept for the
+    MFMA-vs-VALU measurement) meets the same bar as the MFMA path."""
+    wl = W.make(name, overrides=ov, seed=51)
+    if wl.s_aux is not None:
+        wl.s_aux = wl.s_aux * 0.1
+    run_and_check(wl, sink_mode=mode, what=f"VALU tile {name} {ov} {mode}")
+
+
+def test_valu_tile_rejects_other_shapes(valu_engine):
+    for ov in (dict(kv="bf16", q="bf16", out="bf16"), dict(D=64), dict(Hq=64, Hkv=8)):
+        wl = W.make("M0", overrides=dict(B=1, lens=("list", [100]), **ov), seed=52).to(DEV)
+        with pytest.raises(NotImplementedError):
+            W.run(wl)
 
 
 # ---------------------------------------------------------------------------
