@@ -19,7 +19,8 @@ warm-up (300 steps) covers the ~20 ms the shader clock takes to settle under
 load.
 
 Other workloads: ``--config C1..C5`` (decode configurations), ``--config M0b``
-(M0 with bf16 Q, KV and output), ``--config W0..W2`` (the KV write path: a
+(M0 with bf16 Q, KV and output), ``--config G1`` (varlen with sinks at head_dim
+64, Hq=64, Hkv=8), ``--config W0..W2`` (the KV write path: a
 step is one store of a batch of new rows into scattered pages; ``roofline`` is
 the write kernel).  ``--graph`` replays each decode step from a captured HIP
 graph; ``--block-scores`` also computes the pooled 128-token block scores.
@@ -43,13 +44,15 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=300,
                     help="untimed steps first (the shader clock takes ~20 ms of load to settle)")
-    ap.add_argument("--config", default="M0", help="workload name (decode: M0, M0b, C1..C5; KV write: W0..W2)")
+    ap.add_argument("--config", default="M0", help="workload name (decode: M0, M0b, G1, C1..C5; KV write: W0..W2)")
     ap.add_argument("--sets", type=int, default=0, help="input sets to rotate (0: >= 4 and enough for > 1.1 GB)")
     ap.add_argument("--chunk", type=int, default=0, help="split size in tokens (0: library default)")
     ap.add_argument("--block-scores", action="store_true",
                     help="also compute the pooled 128-token block scores in each step")
     ap.add_argument("--qk-engine", choices=["mfma", "valu"], default="mfma",
                     help="QK/PV on the matrix cores (default) or the VALU tile (A/B measurement; f16, D=128)")
+    ap.add_argument("--option", action="append", default=[], metavar="NAME=VALUE",
+                    help="library option (fsk_set_option) set before the run, e.g. head_pairs=0; repeatable")
     ap.add_argument("--graph", action="store_true",
                     help="replay each decode step from a captured HIP graph (no per-step host work)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
@@ -301,6 +304,9 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     nat.set_option("qk_engine", 1 if args.qk_engine == "valu" else 0)
+    for opt in args.option:
+        name, _, value = opt.partition("=")
+        nat.set_option(name, int(value))
     base = W.make(args.config, gen_device=dev, device=dev)
     kv_bytes = base.k.numel() * base.k.element_size() * 2
     n_sets = args.sets or rotation_sets(kv_bytes)
@@ -363,7 +369,7 @@ def main():
     kern_gbs = alg_bytes / (part_avg_ms / 1e3) / 1e9 if part_avg_ms > 0 else None
     traffic_file = args.traffic or os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                                 f"partial_kernel_{args.config}_traffic.md")
-    traffic = (None if (args.chunk or args.graph or args.block_scores or args.qk_engine != "mfma")
+    traffic = (None if (args.chunk or args.graph or args.block_scores or args.qk_engine != "mfma" or args.option)
                else read_traffic(traffic_file))
 
     out = {
@@ -389,6 +395,7 @@ def main():
             "chunk_tokens": args.chunk or "auto",
             "launch": "hip graph replay" if args.graph else "eager",
             "qk_engine": args.qk_engine,
+            "options": args.option,
             "block_scores": bool(args.block_scores),
         },
         "roofline": {

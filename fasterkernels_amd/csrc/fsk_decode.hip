@@ -1517,6 +1517,7 @@ struct Options {
   int target_waves_per_cu = 4;  // automatic split: units of work per CU
   int xcd_skew = 3;             // automatic split: extra share of the even XCDs, in % (see item_of)
   int qk_engine = 0;            // 0: QK and PV on the matrix cores; 1: the VALU tile (A/B measurement)
+  int head_pairs = 1;           // varlen, head_dim 64: neighbouring KV heads as one 128-wide row (see pair_shape)
 } g_opt;
 
 // Event triples of timed decode calls (the partial kernel's start and end and
@@ -1821,7 +1822,8 @@ int run_decode(const Common& c) {
   if (c.chunk < 0 || c.chunk % 32 != 0) return fail(FSK_ERR_INVALID, "chunk_tokens must be 0 or a positive multiple of 32");
   const SplitPlan sp = plan_split(c.layout, c.B, plan_heads(c.layout, c.D, c.Hkv, G), c.kv_extent, c.page_size,
                                   c.chunk, cus);
-  const bool pair = pair_shape(c.layout, c.D, c.Hkv, G) && !c.scores && c.k_sh == 64 && c.v_sh == 64;
+  const bool pair =
+      g_opt.head_pairs && pair_shape(c.layout, c.D, c.Hkv, G) && !c.scores && c.k_sh == 64 && c.v_sh == 64;
   if (c.layout == FSK_LAYOUT_PAGED && sp.chunk_max > kChunkMax)
     return fail(FSK_ERR_UNSUPPORTED, "paged decode takes chunk_tokens <= 2048");
   const int64_t u_max = sp.u_max;
@@ -2028,6 +2030,11 @@ int fsk_set_option(const char* name, int64_t value) {
   if (!strcmp(name, "waves_per_cu")) {
     if (value < 1 || value > 64) return fail(FSK_ERR_INVALID, "waves_per_cu in [1, 64]");
     g_opt.waves_per_cu = (int)value;
+    return FSK_OK;
+  }
+  if (!strcmp(name, "head_pairs")) {
+    if (value != 0 && value != 1) return fail(FSK_ERR_INVALID, "head_pairs is 0 or 1");
+    g_opt.head_pairs = (int)value;
     return FSK_OK;
   }
   if (!strcmp(name, "qk_engine")) {

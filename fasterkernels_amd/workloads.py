@@ -43,6 +43,10 @@ CONFIGS = {
     # fskernels/paged_attn/paged_kv_cache.py:80)
     "M0b": dict(layout="paged", q="bf16", kv="bf16", out="bf16", B=4, Hq=32, Hkv=8, D=128,
                 lens=("fixed", 32768), sinks=False, seed=100),
+    # head_dim 64 with sinks (GPT-OSS-style attention shapes): varlen fp16,
+    # B=4, Hq=64, Hkv=8, 65536 tokens each (the same 537 MB of K/V as M0)
+    "G1": dict(layout="varlen", q="f16", kv="f16", out="f16", B=4, Hq=64, Hkv=8, D=64,
+               lens=("fixed", 65536), sinks=True, seed=106),
 }
 
 DTYPES = {"f16": torch.float16, "bf16": torch.bfloat16, "e4m3": torch.float8_e4m3fn,

@@ -268,6 +268,9 @@ FSK_API int fsk_debug_split(int64_t total, int chunk_min, int chunk_max,
  *   "target_waves_per_cu" automatic split: units of work per CU (default 4)
  *   "xcd_skew"            automatic split: extra share of the even XCDs, in %
  *                         (0..50, default 3; 0 = equal chunks)
+ *   "head_pairs"          1 (default): varlen decodes at head_dim 64 with
+ *                         packed heads read KV heads 2i and 2i+1 as one
+ *                         128-wide row; 0: one KV head per wave
  *   "qk_engine"           0 (default): QK and PV on the matrix cores (MFMA);
  *                         1: the VALU formulation of the tile, for A/B
  *                         measurement (f16 q and KV, head_dim 128, at most 4

@@ -48,6 +48,11 @@ def test_version_and_options(lib):
     assert lib.fsk_set_option(b"chunk_tokens", 0) == nat.FSK_OK
     assert lib.fsk_set_option(b"waves_per_cu", 0) == nat.FSK_ERR_INVALID
     assert lib.fsk_set_option(b"waves_per_cu", 8) == nat.FSK_OK
+    for name in (b"qk_engine", b"head_pairs"):
+        assert lib.fsk_set_option(name, 2) == nat.FSK_ERR_INVALID
+        assert lib.fsk_set_option(name, -1) == nat.FSK_ERR_INVALID
+    assert lib.fsk_set_option(b"qk_engine", 0) == nat.FSK_OK
+    assert lib.fsk_set_option(b"head_pairs", 1) == nat.FSK_OK
 
 
 def test_workspace_bytes(lib):

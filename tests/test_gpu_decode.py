@@ -293,6 +293,19 @@ def test_varlen_d64_head_pairs(Hq, Hkv, kv, mode):
     assert_close(out2, ref, atol, rtol, f"strided heads Hq={Hq} Hkv={Hkv} {kv} {mode}")
 
 
+def test_varlen_d64_head_pairs_option():
+    """head_pairs = 0 keeps one KV head per wave on a pair-eligible shape;
+    both settings match the oracle."""
+    wl = W.make("G1", overrides=dict(B=2, lens=("list", [3000, 70])), seed=44)
+    wl.s_aux = wl.s_aux * 0.1
+    try:
+        nat.set_option("head_pairs", 0)
+        run_and_check(wl, what="G1 shape, head_pairs=0")
+    finally:
+        nat.set_option("head_pairs", 1)
+    run_and_check(wl, what="G1 shape, head_pairs=1")
+
+
 @pytest.mark.parametrize("Hq,Hkv", [(72, 8), (24, 3)])
 def test_varlen_d64_unpaired_shapes(Hq, Hkv):
     """head_dim 64 shapes that keep one KV head per wave: more than 8 query
