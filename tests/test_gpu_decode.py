@@ -513,6 +513,18 @@ def test_batches_above_one_wave(layout):
     run_and_check(wl, chunk_tokens=64, what=f"{layout} B=150 chunk 64")
 
 
+@pytest.mark.parametrize("layout", ["varlen", "paged"])
+def test_maximum_batch(layout):
+    """The largest batch the library takes (16384 sequences): the plan keeps
+    two int32 entries per sequence in LDS (128 KB here), so one workgroup per
+    CU fits; lengths 0..40 with sinks, against the oracle."""
+    name = "C1" if layout == "varlen" else "C3"
+    B = 16384
+    lens = _lens(B, 41, 54)
+    wl = W.make(name, overrides=dict(B=B, Hq=8, Hkv=2, lens=("list", lens), sinks=True), seed=55)
+    run_and_check(wl, what=f"{layout} B={B}")
+
+
 def test_dense_batch_above_one_wave():
     B = 70
     lens = _lens(B, 300, 53)
