@@ -155,10 +155,17 @@ def test_paged_sinks(mode, kv):
     run_and_check(wl, sink_mode=mode, what=f"sinks {mode} {kv}")
 
 
-@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 8), (32, 4), (64, 4), (32, 1), (48, 2)])
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 8), (32, 4), (64, 4), (32, 1), (48, 2), (96, 2), (128, 1)])
 def test_paged_group_sizes(Hq, Hkv):
     wl = W.make("C3", overrides=dict(B=2, Hq=Hq, Hkv=Hkv, lens=("list", [77, 600])), seed=9)
     run_and_check(wl, what=f"G={Hq // Hkv}")
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(96, 2), (128, 1), (40, 8)])
+def test_varlen_large_groups_with_sinks(Hq, Hkv):
+    """Several 16-head blocks per KV head (the last one partly padding), with sinks."""
+    wl = W.make("C1", overrides=dict(B=3, Hq=Hq, Hkv=Hkv, lens=("list", [1, 1500, 333]), sinks=True), seed=10)
+    run_and_check(wl, what=f"varlen G={Hq // Hkv}")
 
 
 @pytest.mark.parametrize("D", [64, 256])
