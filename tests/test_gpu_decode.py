@@ -300,6 +300,14 @@ def test_varlen_d64_head_pairs(Hq, Hkv, kv, mode):
     assert_close(out2, ref, atol, rtol, f"strided heads Hq={Hq} Hkv={Hkv} {kv} {mode}")
 
 
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_varlen_d64_head_pairs_fp8_bf16_query(out):
+    """Head pairs with e4m3 KV and a bf16 query (the C4/C5 dtype mix)."""
+    wl = W.make("C1", overrides=dict(B=3, Hq=64, Hkv=8, D=64, lens=("list", [2500, 3, 700]), kv="e4m3",
+                                      q="bf16", out=out, sinks=True), seed=45)
+    run_and_check(wl, what=f"paired e4m3 KV, bf16 q, out {out}")
+
+
 def test_varlen_d64_head_pairs_option():
     """head_pairs = 0 keeps one KV head per wave on a pair-eligible shape;
     both settings match the oracle."""
