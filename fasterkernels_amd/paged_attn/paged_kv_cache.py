@@ -20,6 +20,7 @@ HIP device.  e4m3 pools (``dtype=torch.float8_e4m3fn``) can carry per-tensor
 """
 from __future__ import annotations
 
+from contextlib import contextmanager
 from dataclasses import dataclass
 from typing import List, Optional, Sequence, Tuple
 
@@ -166,6 +167,46 @@ class PagedKVCache:
             raise RuntimeError("PagedKVCache stores rows with the HIP write kernel; "
                                f"its pools are on {self.k_pool.device}, not a GPU")
 
+    def _new_rows(self, t, name: str, n: int) -> torch.Tensor:
+        """New K or V rows for ``n`` tokens, checked before any bookkeeping
+        changes, on the pools' device: rows on another device (the CPU
+        included) are copied there, as the reference's indexed store copies
+        them (paged_kv_cache.py:128-130)."""
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+        if t.dim() == 4 and t.shape[2] == 1:
+            rows = t.shape[0], t.shape[1], t.shape[3]
+        elif t.dim() == 3:
+            rows = tuple(t.shape)
+        else:
+            raise ValueError(f"{name} must be [n, Hkv, 1, D] or [n, Hkv, D], got {tuple(t.shape)}")
+        if rows != (n, self.num_kv_heads, self.head_dim):
+            raise ValueError(f"{name} holds {tuple(t.shape)} for {n} tokens of "
+                             f"{self.num_kv_heads} heads x {self.head_dim}")
+        if t.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            raise NotImplementedError(f"{name}: dtype {t.dtype} (f16, bf16 or f32 expected)")
+        if t.device != self.k_pool.device:
+            t = t.to(self.k_pool.device)
+        return t
+
+    @contextmanager
+    def _all_or_nothing(self):
+        """Restores the host bookkeeping (lengths, page lists, free list) if
+        the body raises: planning, staging and the launch succeed together or
+        leave no trace.  (The block-table stores ride the write launch, so a
+        call that fails before or at the launch has stored none.)"""
+        lens = list(self._seq_lens)
+        npages = [len(p) for p in self._pages]
+        free = list(self._free_pages)
+        try:
+            yield
+        except BaseException:
+            self._seq_lens[:] = lens
+            for pages, n in zip(self._pages, npages):
+                del pages[n:]
+            self._free_pages[:] = free
+            raise
+
     def _stage(self, slots, updates):
         """One host->device copy of the slots and block-table stores."""
         vals = list(slots)
@@ -196,11 +237,15 @@ class PagedKVCache:
         ([n, Hkv, 1, D] or [n, Hkv, D]) goes to sequence seq_ids[j]; the
         bookkeeping is that of n append_kv calls in order."""
         self._require_gpu()
-        if k.shape[0] != len(seq_ids) or v.shape[0] != len(seq_ids):
-            raise ValueError(f"k/v hold {k.shape[0]}/{v.shape[0]} tokens for {len(seq_ids)} sequences")
-        slots, updates = self._plan(list(seq_ids), 1)
-        slot_dev, upd_dev = self._stage(slots, updates)
-        self._write(layer_idx, k, v, slot_dev, upd_dev)
+        n = len(seq_ids)
+        k = self._new_rows(k, "k", n)
+        v = self._new_rows(v, "v", n)
+        if v.dtype != k.dtype:
+            raise ValueError(f"k and v dtypes differ: {k.dtype} / {v.dtype}")
+        with self._all_or_nothing():
+            slots, updates = self._plan(list(seq_ids), 1)
+            slot_dev, upd_dev = self._stage(slots, updates)
+            self._write(layer_idx, k, v, slot_dev, upd_dev)
 
     def reserve_slots(self, seq_ids: Sequence[int], num_tokens: int = 1) -> torch.Tensor:
         """Takes ``num_tokens`` new positions in each listed sequence (pages as
@@ -208,11 +253,12 @@ class PagedKVCache:
         int64 device tensor [len(seq_ids) * num_tokens], sequence-major, for
         ``write_kv`` of every layer."""
         self._require_gpu()
-        slots, updates = self._plan(list(seq_ids), int(num_tokens))
-        slot_dev, upd_dev = self._stage(slots, updates)
-        if updates:
-            empty = self.k_pool.new_empty((0, self.num_kv_heads, self.head_dim), dtype=torch.float32)
-            self._write(0, empty, empty, slot_dev[:0], upd_dev)
+        with self._all_or_nothing():
+            slots, updates = self._plan(list(seq_ids), int(num_tokens))
+            slot_dev, upd_dev = self._stage(slots, updates)
+            if updates:
+                empty = self.k_pool.new_empty((0, self.num_kv_heads, self.head_dim), dtype=torch.float32)
+                self._write(0, empty, empty, slot_dev[:0], upd_dev)
         return slot_dev
 
     def write_kv(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor):

@@ -105,8 +105,13 @@ def quantize_to_fp8(x):
     return e4m3_encode(y), scale
 
 
+# e4m3_decode of every code, indexed by code (dequantising a large pool is a
+# table lookup; the values are e4m3_decode's own)
+_E4M3_TABLE = e4m3_decode(np.arange(256, dtype=np.uint8))
+
+
 def dequantize_fp8(codes, scale) -> np.ndarray:
-    return (e4m3_decode(codes) * np.float32(scale)).astype(np.float32)
+    return (_E4M3_TABLE[np.asarray(codes, dtype=np.uint8)] * np.float32(scale)).astype(np.float32)
 
 
 # ---------------------------------------------------------------------------

@@ -1,7 +1,13 @@
-// Host-side fuzz of the C ABI argument validation and size arithmetic (no GPU
-// needed: calls that pass validation fail at their first HIP call).  Built with
-// AddressSanitizer and UndefinedBehaviorSanitizer on the host pass by
-// tests/test_capi_sanitizers.py; prints "done" at the end.
+// Host-side fuzz of the C ABI argument validation and size arithmetic.  Many
+// calls start from valid argument sets with fake device addresses, so the fuzz
+// must only ever run where no GPU is visible: there, calls that pass
+// validation fail at their first HIP call; with a device they would launch
+// kernels on those addresses.  main() therefore refuses to run (exit code 3,
+// "device visible") when the HIP runtime reports any device, and
+// tests/test_capi_sanitizers.py hides every device from this process through
+// its environment.  Built with AddressSanitizer and UndefinedBehaviorSanitizer
+// on the host pass; prints "done" at the end.
+#include <hip/hip_runtime_api.h>
 #include <cstdio>
 #include <cstdint>
 #include <cstring>
@@ -31,6 +37,11 @@ static void check(int st, const char* fn) {
   else (void)strlen(e);
 }
 int main() {
+  int devices = 0;
+  if (hipGetDeviceCount(&devices) == hipSuccess && devices > 0) {
+    printf("device visible: the fuzz runs only where no GPU is visible\n");
+    return 3;
+  }
   for (int it = 0; it < 20000; ++it) {
     int64_t n = fsk_workspace_bytes(pick_i(), pick_i(), pick_i(), pick_i(), pick_i(), pick_i64(), pick_i(), pick_i());
     if (n < -4) printf("workspace_bytes %lld\n", (long long)n);

@@ -49,6 +49,14 @@ def assert_close(out, ref, atol, rtol, what=""):
             f"{np.nanmax(np.where(both_nan, 0, err / tol)):.3f}")
 
 
+def exact_np(t):
+    """A tensor as a numpy array holding the same values: f16 stays f16 (the
+    oracle widens each sequence's rows to float64 itself, so a full-size pool
+    is not copied to float64 whole), bf16 and f32 become f32."""
+    t = t.detach().cpu()
+    return t.numpy() if t.dtype == torch.float16 else t.to(torch.float32).numpy()
+
+
 def oracle_for(wl, sink_mode="exp"):
     q = f64(wl.q)
     s_aux = None if wl.s_aux is None else f64(wl.s_aux)
@@ -58,8 +66,8 @@ def oracle_for(wl, sink_mode="exp"):
             vp = wl.v.view(torch.uint8).cpu().numpy()
             return O.decode_paged(q, kp, vp, wl.block_table.cpu().numpy(), wl.lens, s_aux, sink_mode,
                                   float(wl.k_scale), float(wl.v_scale))
-        return O.decode_paged(q, f64(wl.k), f64(wl.v), wl.block_table.cpu().numpy(), wl.lens, s_aux,
-                              sink_mode)
+        return O.decode_paged(q, exact_np(wl.k), exact_np(wl.v), wl.block_table.cpu().numpy(), wl.lens,
+                              s_aux, sink_mode)
     if wl.k_scale is not None:
         k = O.dequantize_fp8(wl.k.view(torch.uint8).cpu().numpy(), float(wl.k_scale))
         v = O.dequantize_fp8(wl.v.view(torch.uint8).cpu().numpy(), float(wl.v_scale))
@@ -444,6 +452,37 @@ def test_single_long_sequence():
 
 def test_c2_full_size_with_sinks():
     run_and_check(W.make("C2"), what="C2")
+
+
+def test_c3_full_size():
+    """Benchmark config C3 as specified: 32 sequences of U[1024, 16384] tokens
+    (297167 in all) on a shuffled pool with 10 % free pages."""
+    wl = W.make("C3")
+    assert wl.B == 32 and min(wl.lens) >= 1024 and max(wl.lens) <= 16384
+    run_and_check(wl, what="C3")
+
+
+def test_c4_full_size():
+    """Benchmark config C4 as specified: e4m3 KV (scale amax/448), bf16 q and
+    output, 4 sequences of 8192 tokens."""
+    wl = W.make("C4")
+    assert wl.lens == [8192] * 4 and wl.k.dtype == torch.float8_e4m3fn and wl.q.dtype == torch.bfloat16
+    run_and_check(wl, what="C4")
+
+
+@pytest.fixture(scope="module")
+def c5_full():
+    return W.make("C5")
+
+
+@pytest.mark.parametrize("mode", ["exp", "linear"])
+def test_c5_full_size(c5_full, mode):
+    """Benchmark config C5 as specified: 64 lognormal-length sequences (16 to
+    32768 tokens, the split-KV load-balance case), e4m3 KV, N(0,1) sinks, in
+    both sink semantics."""
+    wl = c5_full
+    assert wl.B == 64 and min(wl.lens) >= 16 and max(wl.lens) <= 32768 and wl.s_aux is not None
+    run_and_check(wl, sink_mode=mode, what=f"C5 {mode}")
 
 
 # ---------------------------------------------------------------------------

@@ -429,3 +429,31 @@ def test_randomized_writes(seed):
     what = f"seed {seed}: {src}->{pool} scaled={scaled} P={P} ps={ps} hkv={hkv} d={d} n={n}"
     compare(kg, ko, pool, src, "K " + what)
     compare(vg, vo, pool, src, "V " + what)
+
+
+def test_rejected_append_leaves_cache_unchanged_and_host_rows_are_copied():
+    """A rejected append (wrong head count, wrong dtype) changes neither the
+    lengths, the free list nor the device block table; rows given on the CPU
+    are stored as the same rows given on the device are (the reference's
+    indexed store accepts rows from any device)."""
+    gen = torch.Generator().manual_seed(31)
+    cache = PagedKVCache(1, 8, 2, 4, 2, 64, torch.float16, DEV)
+    twin = PagedKVCache(1, 8, 2, 4, 2, 64, torch.float16, DEV)
+    s, t = cache.allocate_sequence(), twin.allocate_sequence()
+    rows = [torch.randn(1, 2, 1, 64, generator=gen).half() for _ in range(2 * 17)]
+    for j in range(17):                      # 17 tokens: the second page is taken
+        cache.append_kv(s, 0, rows[2 * j], rows[2 * j + 1])                  # host rows
+        twin.append_kv(t, 0, rows[2 * j].to(DEV), rows[2 * j + 1].to(DEV))    # device rows
+    torch.cuda.synchronize()
+    lens, free, bt = list(cache._seq_lens), list(cache._free_pages), cache.block_table.clone()
+    with pytest.raises(ValueError):
+        cache.append_kv(s, 0, torch.zeros(1, 3, 1, 64, dtype=torch.float16, device=DEV),
+                        torch.zeros(1, 3, 1, 64, dtype=torch.float16, device=DEV))
+    with pytest.raises(NotImplementedError):
+        cache.append_kv(s, 0, torch.zeros(1, 2, 1, 64, dtype=torch.int32, device=DEV),
+                        torch.zeros(1, 2, 1, 64, dtype=torch.int32, device=DEV))
+    torch.cuda.synchronize()
+    assert cache._seq_lens == lens and cache._free_pages == free
+    assert torch.equal(cache.block_table, bt)
+    assert torch.equal(cache.block_table, twin.block_table) and cache._seq_lens == twin._seq_lens
+    assert torch.equal(cache.k_pool.cpu(), twin.k_pool.cpu()) and torch.equal(cache.v_pool.cpu(), twin.v_pool.cpu())

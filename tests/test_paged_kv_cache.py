@@ -175,6 +175,60 @@ def test_row_stores_refuse_host_pools():
     assert c._seq_lens[s] == 0 and c.pages_free == 8   # nothing was planned
 
 
+def _host_state(c):
+    return list(c._seq_lens), [list(p) for p in c._pages], list(c._free_pages), c.block_table.clone()
+
+
+@pytest.mark.parametrize("fail_at", ["_stage", "_write"])
+def test_failed_append_leaves_no_trace(monkeypatch, fail_at):
+    """An append or reservation whose staging or launch fails restores the
+    lengths, page lists and free list (the block-table stores ride the failed
+    launch, so the device table is untouched too).  The GPU-only steps are
+    stood in for by host functions here; one of them raises."""
+    c = make()
+    s0, s1 = c.allocate_sequence(), c.allocate_sequence()
+    monkeypatch.setattr(c, "_require_gpu", lambda: None)
+    monkeypatch.setattr(c, "_stage", lambda slots, upd: (torch.tensor(slots), torch.tensor(upd).view(-1, 2)))
+    monkeypatch.setattr(c, "_write", lambda *a: None)
+    k = torch.zeros(2, 2, 1, 8, dtype=torch.float16)
+    c.append_kv_batch([s0, s1], 0, k, k)          # one page each
+    c.reserve_slots([s0], 20)                      # crosses into a second page
+    before = _host_state(c)
+
+    def boom(*a, **kw):
+        raise RuntimeError("launch failed")
+    monkeypatch.setattr(c, fail_at, boom)
+    with pytest.raises(RuntimeError, match="launch failed"):
+        c.append_kv_batch([s1, s0, s1], 0, torch.zeros(3, 2, 1, 8), torch.zeros(3, 2, 1, 8))
+    with pytest.raises(RuntimeError, match="launch failed"):
+        c.reserve_slots([s0, s1], 40)
+    after = _host_state(c)
+    assert after[:3] == before[:3] and torch.equal(after[3], before[3])
+
+
+def test_rejected_rows_leave_no_trace(monkeypatch):
+    """k/v of the wrong shape, head count or dtype raise before any page
+    bookkeeping changes."""
+    c = make()
+    s = c.allocate_sequence()
+    monkeypatch.setattr(c, "_require_gpu", lambda: None)
+    before = _host_state(c)
+    good = torch.zeros(1, 2, 1, 8, dtype=torch.float16)
+    for k, err in ((torch.zeros(1, 3, 1, 8, dtype=torch.float16), ValueError),   # Hkv 3, cache has 2
+                   (torch.zeros(1, 2, 1, 4, dtype=torch.float16), ValueError),   # head_dim 4
+                   (torch.zeros(2, 2, 1, 8, dtype=torch.float16), ValueError),   # two tokens, one sequence
+                   (torch.zeros(1, 2, 2, 8, dtype=torch.float16), ValueError),   # two positions
+                   (torch.zeros(1, 2, 1, 8, dtype=torch.int32), NotImplementedError)):
+        with pytest.raises(err):
+            c.append_kv(s, 0, k, good)
+        with pytest.raises(err):
+            c.append_kv(s, 0, good, k)
+    with pytest.raises(ValueError, match="dtypes differ"):
+        c.append_kv(s, 0, good, good.float())
+    after = _host_state(c)
+    assert after[:3] == before[:3] and torch.equal(after[3], before[3])
+
+
 def test_scales_only_for_e4m3_pools():
     with pytest.raises(ValueError):
         PagedKVCache(1, 2, 1, 1, 1, 8, torch.float16, "cpu", k_scale=0.5, v_scale=0.5)
