@@ -10,11 +10,15 @@ rotated, with a footprint above 1.1 GB, beyond the 256 MB Infinity Cache.
 Prints one JSON line.  ``value`` is the achieved algorithmic HBM bandwidth of a
 whole step (valid K+V bytes + Q + output + block-table entries + lengths) in
 GB/s; ``us_per_step`` and ``pct_of_peak`` (of 8 TB/s) are reported beside it.
+``ms_per_step`` is the mean over the K timed steps (one wall-clock interval
+between synchronisations); ``us_per_step_median`` is the median over groups of
+10 steps of a following pass, from HIP events between the groups.
 ``roofline`` is the split-KV partial kernel alone, timed with HIP events that
-its own dispatches stamp (hipExtLaunchKernel) on every call of a second
-pass of the same steps that follows the timed steps: the timing costs host
-time per call, so the step timing runs without it.  ``cpu_baseline`` times
-the CPU oracle on a bounded sample of the same workload.  The default
+its own dispatches stamp (hipExtLaunchKernel) on every call of a further
+pass of the same steps: the timing costs host time per call, so the step
+timing runs without it.  ``cpu_baseline`` times the reference's PyTorch
+decode path restated on the host (oracle/torch_ref.py) in the inputs' own
+dtypes over the same workload, median of >= 3 runs, with the thread count.  The default
 warm-up (300 steps) covers the ~20 ms the shader clock takes to settle under
 load.
 
@@ -104,108 +108,149 @@ def read_traffic(path: str):
 KT_EVERY = 1
 
 
+def median_step_us(step, first: int, steps: int, group: int = 10) -> float:
+    """Median step time in µs: HIP events on the current stream between groups
+    of ``group`` consecutive steps, over a pass of ``steps`` steps (at least 3
+    groups) that follows the timed ones (each record costs host time, so the
+    timed steps run without them).  Returns the median over groups of each
+    group's time per step."""
+    import torch
+
+    n_groups = max(3, steps // group)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n_groups + 1)]
+    i = first
+    evs[0].record()
+    for g in range(n_groups):
+        for _ in range(group):
+            step(i)
+            i += 1
+        evs[g + 1].record()
+    torch.cuda.synchronize()
+    return statistics.median(evs[g].elapsed_time(evs[g + 1]) * 1e3 / group for g in range(n_groups))
+
+
 def kernel_timing_steps(steps: int) -> int:
     """Length of the kernel-timing pass that follows the timed steps (>= 50 samples)."""
     return KT_EVERY * max(steps // KT_EVERY, 50)
 
 
-def cpu_baseline(wl, budget_s: float):
-    """Times the numpy oracle on the first sequence of ``wl`` (bounded sample)."""
-    import numpy as np
-    import torch
+def host_threads():
+    """Threads for the CPU baseline: the process's affinity mask, capped at
+    OMP_NUM_THREADS when that is set (a GPU box sets it to the CPU share it
+    gives one GPU).  Returns (threads, cpus in the affinity mask)."""
+    n_aff = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    n = min(n_aff, int(cap)) if cap.isdigit() and int(cap) > 0 else n_aff
+    return n, n_aff
 
-    from oracle import decode_oracle as O
 
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover - threadpoolctl missing
-        threads = 1
-    L = wl.lens[0]
-    q = wl.q[:1].float().cpu().numpy()
-    if wl.layout == "paged":
-        npg = (L + 15) // 16
-        pages = wl.block_table[0, :npg].long()
-        k = wl.k[pages].cpu()
-        v = wl.v[pages].cpu()
-        bt = np.arange(npg, dtype=np.int64)[None, :]
-        kw = {}
-        if wl.k_scale is not None:
-            k, v = k.view(torch.uint8).numpy(), v.view(torch.uint8).numpy()
-            kw = dict(k_scale=float(wl.k_scale), v_scale=float(wl.v_scale))
-        else:
-            k, v = k.float().numpy(), v.float().numpy()
-        s_aux = None if wl.s_aux is None else wl.s_aux.cpu().numpy()
-
-        def step():
-            O.decode_paged(q, k, v, bt, [L], s_aux, "exp", **kw)
-    else:
-        k = wl.k[: L].float().cpu().numpy()
-        v = wl.v[: L].float().cpu().numpy()
-        cu = np.array([0, L])
-        s_aux = None if wl.s_aux is None else wl.s_aux.cpu().numpy()
-
-        def step():
-            O.decode_varlen(q, k, v, cu, s_aux)
-    step()  # warm-up
+def _median_runs(fn, budget_s: float, min_runs: int = 3, max_runs: int = 50):
+    """Median of >= min_runs timed calls of fn after one warm-up call, within
+    about budget_s seconds.  Returns (median seconds, runs)."""
+    fn()  # warm-up
     times = []
     t_end = time.perf_counter() + budget_s
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+    while len(times) < min_runs or (time.perf_counter() < t_end and len(times) < max_runs):
         t0 = time.perf_counter()
-        step()
+        fn()
         times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    kv_bytes = L * wl.Hkv * wl.D * 2 * wl.k.element_size()
-    sample_bytes = kv_bytes + wl.Hq * wl.D * (wl.q.element_size() + 2)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(wl, budget_s: float):
+    """The reference's PyTorch decode path on the host (oracle/torch_ref.py:
+    per-sequence gather, fp8 dequantisation, repeat_kv, matmul, softmax,
+    matmul), timed over the whole step in the inputs' own dtypes, with an
+    fp32-upcast variant beside it.  Median of >= 3 runs after a warm-up."""
+    import torch
+
+    from oracle import torch_ref as R
+
+    threads, n_aff = host_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    cpu = lambda t: None if t is None else t.detach().cpu()  # noqa: E731
+    q, k, v = cpu(wl.q), cpu(wl.k), cpu(wl.v)
+    kw = dict(block_table=cpu(wl.block_table), cu_seqlens=cpu(wl.cu_seqlens), s_aux=cpu(wl.s_aux),
+              k_scale=cpu(wl.k_scale), v_scale=cpu(wl.v_scale))
+    alg = wl.algorithmic_bytes()
+    compute = q.dtype  # f16 / bf16: the query's dtype, fp8 KV widened to it
+    try:
+        # the whole step when a run fits a quarter of the budget, else the
+        # first sequences that do (timed, then scaled by their share of tokens)
+        t0 = time.perf_counter()
+        R.decode(q, k, v, wl.lens, seqs=[0], **kw)
+        per_token = (time.perf_counter() - t0) / max(wl.lens[0], 1)
+        seqs, tok = [], 0
+        for b, L in enumerate(wl.lens):
+            if seqs and (tok + L) * per_token > budget_s / 4:
+                break
+            seqs.append(b)
+            tok += L
+        share = tok / max(wl.total_tokens, 1)
+        med, runs = _median_runs(lambda: R.decode(q, k, v, wl.lens, seqs=seqs, **kw), budget_s * 2 / 3)
+        med32, runs32 = _median_runs(
+            lambda: R.decode(q, k, v, wl.lens, seqs=seqs, compute_dtype=torch.float32, **kw), budget_s / 3)
+    finally:
+        torch.set_num_threads(prev)
+    us_step = med / share * 1e6
+    us_step32 = med32 / share * 1e6
+    dt = str(compute).replace("torch.", "")
+    sample = (f"the whole step ({wl.B} sequences, {wl.total_tokens} tokens)" if len(seqs) == wl.B else
+              f"sequences 0..{len(seqs) - 1} of {wl.B} ({tok} of {wl.total_tokens} tokens), scaled to the step")
     return {
-        "value": round(sample_bytes / med / 1e9, 4),
+        "value": round(alg / (us_step * 1e-6) / 1e9, 3),
         "unit": "GB/s",
-        "us_per_step_extrapolated": round(med * 1e6 * wl.B, 1),
+        "us_per_step": round(us_step, 1),
         "cores": threads,
+        "affinity_cpus": n_aff,
         "kind": "port",
-        "sample": f"numpy float64 oracle, sequence 0 of {wl.name} ({L} tokens, {wl.Hq} q heads), "
-                  f"median of {len(times)} runs",
+        "dtype": dt,
+        "sample": f"host torch restatement of the reference's PyTorch decode path (per-sequence gather, "
+                  f"repeat_kv, matmul, softmax, matmul in {dt}{', fp8 dequantised to ' + dt if wl.k_scale is not None else ''}) "
+                  f"over {sample}, median of {runs} runs after a warm-up",
+        "fp32_upcast": {"value": round(alg / (us_step32 * 1e-6) / 1e9, 3), "unit": "GB/s",
+                        "us_per_step": round(us_step32, 1), "runs": runs32},
     }
 
 
 def cpu_baseline_write(wl, budget_s: float):
-    """Times the numpy oracle's row store on a bounded sample of ``wl``'s tokens."""
-    import numpy as np
+    """The reference's row store on the host: the indexed assignment of
+    fskernels/paged_attn/paged_kv_cache.py:128-130 (pool[page, :, row, :] =
+    rows) for every token of the step at once, with the fixed-scale e4m3
+    quantiser for scaled pools.  Median of >= 3 runs after a warm-up."""
     import torch
 
-    from oracle import decode_oracle as O
+    threads, n_aff = host_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    k, v, slots = wl.k.cpu(), wl.v.cpu(), wl.slots.cpu()
+    kp, vp = wl.k_pool.cpu(), wl.v_pool.cpu()
+    pages, rows = slots // 16, slots % 16
+    ks = None if wl.k_scale is None else wl.k_scale.cpu()
+    vs = None if wl.v_scale is None else wl.v_scale.cpu()
 
-    n = min(wl.tokens, 2048)
-    x_k = wl.k[:n].float().cpu().numpy()
-    x_v = wl.v[:n].float().cpu().numpy()
-    slots = wl.slots[:n].cpu().numpy()
-    pool_dt = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float8_e4m3fn: "e4m3"}[wl.k_pool.dtype]
-    shape = tuple(wl.k_pool.shape)
-    kp = np.zeros(shape, dtype=O._POOL_NP[pool_dt])
-    vp = np.zeros_like(kp)
-    ks = None if wl.k_scale is None else np.float32(wl.k_scale.item())
-    vs = None if wl.v_scale is None else np.float32(wl.v_scale.item())
+    def store(pool, x, scale):
+        if scale is not None:
+            x = (x.float() / scale).clamp(-448.0, 448.0)
+        pool[pages, :, rows, :] = x.to(pool.dtype)
 
     def step():
-        O.paged_write(kp, slots, x_k, pool_dt, ks)
-        O.paged_write(vp, slots, x_v, pool_dt, vs)
-    step()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    per_tok = wl.k.shape[1] * wl.k.shape[2] * 2 * (wl.k.element_size() + wl.k_pool.element_size()) + 8
+        store(kp, k, ks)
+        store(vp, v, vs)
+    try:
+        med, runs = _median_runs(step, budget_s)
+    finally:
+        torch.set_num_threads(prev)
     return {
-        "value": round(n * per_tok / med / 1e9, 4),
+        "value": round(wl.algorithmic_bytes() / med / 1e9, 3),
         "unit": "GB/s",
-        "us_per_step_extrapolated": round(med * 1e6 * wl.tokens / n, 1),
-        "cores": 1,
+        "us_per_step": round(med * 1e6, 1),
+        "cores": threads,
+        "affinity_cpus": n_aff,
         "kind": "port",
-        "sample": f"numpy oracle row store, first {n} of {wl.tokens} tokens of {wl.name}, "
-                  f"median of {len(times)} runs",
+        "sample": f"host torch indexed store of all {wl.tokens} tokens of {wl.name} "
+                  f"(the reference's append_kv assignment, batched), median of {runs} runs after a warm-up",
     }
 
 
@@ -231,6 +276,7 @@ def bench_write(args):
         W.run_write(sets[i % n_sets])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    med_us = median_step_us(lambda i: W.run_write(sets[i % n_sets]), args.steps, args.steps)
     # kernel duration: a second timed pass of the same steps, the write kernels
     # stamped by their own dispatches (the hook costs host time, so it stays
     # out of the step timing above)
@@ -249,6 +295,7 @@ def bench_write(args):
         "value": round(gbs, 2),
         "unit": "GB/s",
         "us_per_step": round(ms_step * 1e3, 2),
+        "us_per_step_median": round(med_us, 2),
         "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
         "n_gpus": 1,
         "steps": args.steps,
@@ -334,6 +381,7 @@ def main():
         step(i)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    med_us = median_step_us(step, args.steps, args.steps)
     # Kernel durations: a second timed pass of the same steps, with timing on
     # the calls KT_EVERY selects (the timing costs host time, so it stays out
     # of the step timing above).
@@ -378,6 +426,7 @@ def main():
         "value": round(gbs, 2),
         "unit": "GB/s",
         "us_per_step": round(ms_step * 1e3, 2),
+        "us_per_step_median": round(med_us, 2),
         "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
         "n_gpus": 1,
         "steps": args.steps,

@@ -528,3 +528,112 @@ def test_planted_mistake_is_caught(name, monkeypatch):
 
     failed = [p.__name__ for p in PINS if not holds(p)]
     assert failed, f"no pin caught the planted mistake: {name}"
+
+
+# ---------------------------------------------------------------------------
+# the host torch restatement timed as the CPU baseline (oracle/torch_ref.py)
+# ---------------------------------------------------------------------------
+from oracle import torch_ref as R  # noqa: E402
+
+
+def _torch_ref_case(layout, fp8, sinks, seed):
+    """A small seeded batch in both forms: torch tensors for torch_ref, numpy
+    for the float64 oracle (pools of 16-token pages scattered by a
+    permutation, or packed rows with cu_seqlens)."""
+    g = np.random.default_rng(seed)
+    Hq, Hkv, D, lens = 8, 2, 32, [1, 17, 40, 5]
+    B = len(lens)
+    q = g.standard_normal((B, Hq, D)).astype(np.float32)
+    s_aux = g.standard_normal(Hq).astype(np.float32) if sinks else None
+    case = dict(q=q, lens=lens, s_aux=s_aux)
+    if layout == "paged":
+        npg = [(L + 15) // 16 for L in lens]
+        P = sum(npg) + 2
+        perm = g.permutation(P)
+        bt = np.full((B, max(npg)), -1, np.int32)
+        off = 0
+        for b, n in enumerate(npg):
+            bt[b, :n] = perm[off:off + n]
+            off += n
+        shape = (P, Hkv, 16, D)
+        case.update(block_table=bt)
+    else:
+        cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        shape = (int(cu[-1]), Hkv, D)
+        case.update(cu_seqlens=cu)
+    k = g.standard_normal(shape).astype(np.float32)
+    v = g.standard_normal(shape).astype(np.float32)
+    if fp8:
+        k8, ks = O.quantize_to_fp8(k)
+        v8, vs = O.quantize_to_fp8(v)
+        case.update(k=k8, v=v8, k_scale=float(ks), v_scale=float(vs))
+    else:
+        case.update(k=k, v=v)
+    return case
+
+
+def _run_torch_ref(case, sink_mode, compute_dtype):
+    fp8 = "k_scale" in case
+    t = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
+    k, v = t(case["k"]), t(case["v"])
+    if fp8:
+        k, v = k.view(torch.float8_e4m3fn), v.view(torch.float8_e4m3fn)
+    return R.decode(t(case["q"]).to(compute_dtype), k, v, case["lens"],
+                    block_table=t(case.get("block_table")), cu_seqlens=t(case.get("cu_seqlens")),
+                    s_aux=t(case["s_aux"]), sink_mode=sink_mode,
+                    k_scale=torch.tensor(case["k_scale"]) if fp8 else None,
+                    v_scale=torch.tensor(case["v_scale"]) if fp8 else None,
+                    compute_dtype=compute_dtype)
+
+
+def _numpy_oracle(case, sink_mode):
+    q = case["q"].astype(np.float64)
+    s_aux = case["s_aux"]
+    ks, vs = case.get("k_scale"), case.get("v_scale")
+    if "block_table" in case:
+        return O.decode_paged(q, case["k"], case["v"], case["block_table"], case["lens"], s_aux, sink_mode, ks, vs)
+    k, v = case["k"], case["v"]
+    if ks is not None:
+        k, v = O.dequantize_fp8(k, ks), O.dequantize_fp8(v, vs)
+    return O.decode_varlen(q, k, v, case["cu_seqlens"], s_aux, sink_mode)
+
+
+@pytest.mark.parametrize("layout", ["paged", "varlen"])
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("sink_mode", [None, "exp", "linear"])
+def test_torch_ref_matches_oracle(layout, fp8, sink_mode):
+    """The CPU baseline's torch path computes the oracle's attention: to fp32
+    rounding in float32, and to f16 / bf16 rounding in the inputs' dtypes."""
+    case = _torch_ref_case(layout, fp8, sink_mode is not None, seed=3 + 2 * fp8)
+    if sink_mode == "linear":
+        # den = sum + z: a negative z can cancel most of a short sequence's
+        # sum and amplify any rounding, so the half-precision comparison
+        # uses non-negative sinks (float32 has the margin either way)
+        case["s_aux"] = np.abs(case["s_aux"])
+    mode = sink_mode or "exp"
+    want = _numpy_oracle(case, mode)
+    for dt, tol in ((torch.float32, 1e-5), (torch.float16, 4e-3), (torch.bfloat16, 3e-2)):
+        got = _run_torch_ref(case, mode, dt).double().numpy()
+        assert np.allclose(got, want, atol=tol, rtol=tol), (dt, np.abs(got - want).max())
+
+
+def test_torch_ref_repeat_kv_and_mistakes_are_caught(monkeypatch):
+    """repeat_kv maps query head h to KV head h // G (a planted h % Hkv map
+    and a transposed page index fail the comparison above)."""
+    x = torch.arange(2 * 3 * 4, dtype=torch.float32).view(2, 3, 4)
+    r = R.repeat_kv(x, 3)
+    assert r.shape == (6, 3, 4) and all(torch.equal(r[h], x[h // 3]) for h in range(6))
+    case = _torch_ref_case("paged", False, True, seed=11)
+    want = _numpy_oracle(case, "exp")
+    good = _run_torch_ref(case, "exp", torch.float32).double().numpy()
+    assert np.allclose(good, want, atol=1e-5)
+    monkeypatch.setattr(R, "repeat_kv", lambda t, n: t.repeat(n, 1, 1))          # h % Hkv
+    assert not np.allclose(_run_torch_ref(case, "exp", torch.float32).double().numpy(), want, atol=1e-3)
+    monkeypatch.undo()
+
+    def transposed_rows(k, b, length, *, block_table=None, cu_seqlens=None):
+        n = (length + 15) // 16
+        rows = k[block_table[b, :n].long()]
+        return rows.permute(1, 2, 0, 3).reshape(rows.shape[1], n * 16, rows.shape[3])[:, :length]
+    monkeypatch.setattr(R, "sequence_rows", transposed_rows)                       # t % 16 / t // 16 swapped
+    assert not np.allclose(_run_torch_ref(case, "exp", torch.float32).double().numpy(), want, atol=1e-3)
