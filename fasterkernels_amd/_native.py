@@ -48,6 +48,8 @@ SIGNATURES = {
     "fsk_decode_paged": (_I, [_P, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _I, _P, _I, _I,
                               _P, _I, _P, _P, _P, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _P, _L,
                               _I, _P]),
+    "fsk_decode_paged_noalloc": (_I, [_P, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _I, _P, _I, _I,
+                                      _P, _I, _P, _P, _P, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P]),
     "fsk_decode_dense": (_I, [_P, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _L, _P, _P, _P, _I, _P,
                               _P, _P, _P, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _P, _L, _I, _P]),
     "fsk_score_workspace_bytes": (_L, [_I, _I, _I]),

@@ -30,10 +30,20 @@
 #include <algorithm>
 #include <cmath>
 #include <string.h>
+#include <mutex>
 #include <string>
 #include <vector>
 
 #include "fsk_decode.h"
+
+// Device scratch of the allocation-free entry point fsk_decode_paged_noalloc:
+// the decode workspace (plan, partial maxima/sums, partial outputs) lives in
+// this file-scope array instead of caller- or library-allocated memory.  Every
+// device the library runs on holds its own copy (FSK_NOALLOC_SCRATCH_BYTES)
+// from the first call on that device until the process ends.  In host code
+// the name is only a host-side stand-in: the device address comes from
+// hipGetSymbolAddress, once per device (see noalloc_scratch).
+static __device__ __align__(256) uint8_t scratch[FSK_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -1679,6 +1689,7 @@ struct Common {
   void* ws; int64_t ws_bytes; int chunk;
   hipStream_t stream;
   void* scores; int nblk;  // block scores [B, Hq, nblk] in the output dtype, or null
+  bool no_timing;          // never stamp this call (no event creation: the allocation-free entry)
 };
 
 bool aligned(const void* p, int a) { return ((uintptr_t)p % a) == 0; }
@@ -1878,8 +1889,8 @@ int run_decode(const Common& c) {
   (void)hipGetLastError();
   // Timed calls: the partial kernel's dispatch stamps its start and end, the
   // reduce's its end (no separate event records around the launches).
-  hipEvent_t ev[3];
-  timing_events(ev);
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+  if (!c.no_timing) timing_events(ev);
   int rc;
   const bool sc = c.scores != nullptr;
   const Launch lp{c.stream, ev[0], ev[1]};
@@ -2212,6 +2223,79 @@ int fsk_decode_paged(const void* q, int64_t q_stride_b, int64_t q_stride_h, cons
   c.B = batch; c.Hq = num_q_heads; c.Hkv = num_kv_heads; c.D = head_dim;
   c.q_dt = q_dtype; c.kv_dt = kv_dtype; c.o_dt = out_dtype; c.sm_scale = sm_scale;
   c.ws = workspace; c.ws_bytes = workspace_bytes; c.chunk = chunk_tokens; c.stream = (hipStream_t)stream;
+  return run_decode(c);
+}
+
+}  // extern "C"
+
+namespace {
+// Device address of `scratch` on the current device, looked up once per device
+// (with that device current) and kept; null on failure (g_err says why).
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {nullptr};
+
+void* noalloc_scratch() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    fail(FSK_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= 64) {
+    fail(FSK_ERR_UNSUPPORTED, "device index above 63");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      fail(FSK_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" {
+
+int fsk_decode_paged_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_pool,
+                             int64_t k_stride_p, int64_t k_stride_h, int64_t k_stride_t, const void* v_pool,
+                             int64_t v_stride_p, int64_t v_stride_h, int64_t v_stride_t,
+                             const int32_t* block_table, int64_t bt_stride_b, int max_blocks,
+                             const int32_t* seq_lens, int num_pages, int page_size, const float* s_aux,
+                             int sink_mode, const float* k_scale, const float* v_scale, void* out,
+                             int64_t o_stride_b, int64_t o_stride_h, int batch, int num_q_heads,
+                             int num_kv_heads, int head_dim, int q_dtype, int kv_dtype, int out_dtype,
+                             float sm_scale, int chunk_tokens, void* stream) {
+  // The workspace this call needs, from the same sizing as fsk_workspace_bytes
+  // (argument errors are reported by the decode's own validation below).
+  const int64_t need = fsk_workspace_bytes(FSK_LAYOUT_PAGED, batch, num_q_heads, num_kv_heads, head_dim,
+                                           max_blocks, page_size, chunk_tokens);
+  if (need < 0) return (int)need;
+  if (need > (int64_t)FSK_NOALLOC_SCRATCH_BYTES)
+    return fail(FSK_ERR_UNSUPPORTED, "fsk_decode_paged_noalloc: this call needs " + std::to_string(need) +
+                                         " bytes of workspace, above the " +
+                                         std::to_string((long long)FSK_NOALLOC_SCRATCH_BYTES) +
+                                         "-byte device scratch; use fsk_decode_paged with a workspace");
+  void* ws = noalloc_scratch();
+  if (!ws) return FSK_ERR_HIP;
+  Common c;
+  memset(&c, 0, sizeof(c));
+  c.layout = FSK_LAYOUT_PAGED;
+  c.q = q; c.q_sb = q_stride_b; c.q_sh = q_stride_h;
+  c.k = k_pool; c.k_s0 = k_stride_p; c.k_sh = k_stride_h; c.k_st = k_stride_t;
+  c.v = v_pool; c.v_s0 = v_stride_p; c.v_sh = v_stride_h; c.v_st = v_stride_t;
+  c.bt = block_table; c.bt_sb = bt_stride_b; c.max_blocks = max_blocks;
+  c.lens = seq_lens; c.num_pages = num_pages; c.page_size = page_size; c.kv_extent = max_blocks;
+  c.s_aux = s_aux; c.sink_mode = sink_mode; c.k_scale = k_scale; c.v_scale = v_scale;
+  c.out = out; c.o_sb = o_stride_b; c.o_sh = o_stride_h;
+  c.B = batch; c.Hq = num_q_heads; c.Hkv = num_kv_heads; c.D = head_dim;
+  c.q_dt = q_dtype; c.kv_dt = kv_dtype; c.o_dt = out_dtype; c.sm_scale = sm_scale;
+  c.ws = ws; c.ws_bytes = FSK_NOALLOC_SCRATCH_BYTES; c.chunk = chunk_tokens; c.stream = (hipStream_t)stream;
+  c.no_timing = true;
   return run_decode(c);
 }
 

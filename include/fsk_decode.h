@@ -126,6 +126,37 @@ FSK_API int fsk_decode_paged(const void *q, int64_t q_stride_b, int64_t q_stride
                      void *workspace, int64_t workspace_bytes, int chunk_tokens,
                      void *stream);
 
+/* Allocation-free paged decode.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP-graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and
+ * results as fsk_decode_paged, without workspace / workspace_bytes: the
+ * workspace is a device array inside the library of
+ * FSK_NOALLOC_SCRATCH_BYTES bytes per device, held from the first call on a
+ * device until the process ends.  The call allocates nothing and frees
+ * nothing.  It returns FSK_ERR_UNSUPPORTED, launching nothing, when the shape
+ * needs more workspace than that (fsk_workspace_bytes(FSK_LAYOUT_PAGED, ...)
+ * tells how much; the M0 shape, B=4 x 32768 tokens, Hq=32, Hkv=8, D=128,
+ * needs 8.6 MB).  Every call on one device shares that device's array:
+ * calls that overlap on one device (two streams, two threads, or two entries
+ * of one graph that may run concurrently) race and give wrong results;
+ * serialise them.  Nothing in the array needs to start at zero (each call
+ * writes its plan and every partial its reduce reads), so no clearing is
+ * issued. */
+#define FSK_NOALLOC_SCRATCH_BYTES (32ll << 20)
+FSK_API int fsk_decode_paged_noalloc(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                     const void *k_pool, int64_t k_stride_p, int64_t k_stride_h,
+                     int64_t k_stride_t,
+                     const void *v_pool, int64_t v_stride_p, int64_t v_stride_h,
+                     int64_t v_stride_t,
+                     const int32_t *block_table, int64_t bt_stride_b, int max_blocks,
+                     const int32_t *seq_lens, int num_pages, int page_size,
+                     const float *s_aux, int sink_mode,
+                     const float *k_scale, const float *v_scale,
+                     void *out, int64_t o_stride_b, int64_t o_stride_h,
+                     int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                     int q_dtype, int kv_dtype, int out_dtype, float sm_scale,
+                     int chunk_tokens, void *stream);
+
 /* Block scores: the varlen / paged decode plus, per sequence b, query head h
  * and 128-token block j of the sequence, the largest final attention
  * probability of a token of that block:
