@@ -258,7 +258,7 @@ def bench_write(args):
     """The KV write path: one store of a batch of rows into scattered pages."""
     import torch
 
-    from fasterkernels_amd import _native as nat
+    from fasterkernels_amd import native as nat
     from fasterkernels_amd import workloads as W
 
     dev = torch.device("cuda", 0)
@@ -339,7 +339,7 @@ def main():
         sys.exit(2)
     import torch
 
-    from fasterkernels_amd import _native as nat
+    from fasterkernels_amd import native as nat
     from fasterkernels_amd import workloads as W
 
     if not torch.cuda.is_available():
@@ -364,7 +364,7 @@ def main():
     alg_bytes = base.algorithmic_bytes()
 
     if args.graph:
-        from fasterkernels_amd.graph import DecodeGraph
+        from fskernels.engine.hip_graph import DecodeGraph
         graphs = [DecodeGraph(W.run, s, chunk_tokens=args.chunk, block_scores=args.block_scores) for s in sets]
 
         def step(i):

@@ -197,7 +197,7 @@ def make(name: str = "M0", *, device=None, seed: int | None = None, overrides: d
 def run(wl: Workload, *, sink_mode: str = "exp", chunk_tokens: int = 0, block_scores: bool = False):
     """One decode step of ``wl`` through the HIP entry points (with
     ``block_scores``: also the pooled block scores, returned as (out, S))."""
-    from .hip import decode as dec
+    from fskernels.hip import decode as dec
     if wl.layout == "paged":
         return dec.paged_flash_decode(wl.q, wl.k, wl.v, wl.block_table, wl.seq_lens, PAGE,
                                       s_aux=wl.s_aux, k_scale=wl.k_scale, v_scale=wl.v_scale,
@@ -274,5 +274,5 @@ def make_write(name: str, *, device, data_seed: int | None = None) -> WriteWorkl
 
 def run_write(wl: WriteWorkload) -> None:
     """One store of ``wl``'s rows through the HIP write entry point."""
-    from .hip.kv_write import paged_kv_write
+    from fskernels.hip.kv_write import paged_kv_write
     paged_kv_write(wl.k, wl.v, wl.k_pool, wl.v_pool, wl.slots, k_scale=wl.k_scale, v_scale=wl.v_scale)

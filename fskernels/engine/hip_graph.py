@@ -5,7 +5,7 @@ tens of microseconds of host work (argument checks, ctypes, two or three
 launches).  Capturing the step once and replaying it leaves one graph launch
 per step.  The reference does this for a whole HF model
 (fskernels/engine/cuda_graph_runner.py:97-237, see
-fasterkernels_amd.engine.HIPGraphRunner); this module does it for the decode
+fskernels.engine.HIPGraphRunner); this module does it for the decode
 hot path itself:
 
 * ``DecodeGraph`` captures any call of the decode / KV-write entry points.
@@ -27,9 +27,9 @@ from typing import Callable, List, Optional, Sequence
 
 import torch
 
-from .hip.decode import paged_flash_decode
-from .hip.kv_write import paged_kv_write
-from .paged_attn.paged_kv_cache import PAGE_SIZE, PagedKVCache
+from ..hip.decode import paged_flash_decode
+from ..hip.kv_write import paged_kv_write
+from ..paged_attn.paged_kv_cache import PAGE_SIZE, PagedKVCache
 
 
 class DecodeGraph:

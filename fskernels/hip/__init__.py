@@ -1,4 +1,6 @@
-"""The single HIP backend of the decode hot path (gfx950)."""
+"""The single HIP backend of the decode hot path (gfx950): it replaces the
+reference's fskernels.triton, fskernels.cuda and fskernels.tilelang decode
+modules.  The HF attention patches are in fskernels.hip.hf."""
 from .decode import (FP8_DTYPE, FP8_MAX, flash_decode_gqa_hf_dense_optimized,
                      flash_decode_gqa_hf_fp8, flash_decode_gqa_varlen, fp8_decode_table,
                      paged_flash_decode, paged_gather, quantize_to_fp8, set_num_splits,

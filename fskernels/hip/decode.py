@@ -13,7 +13,7 @@ import math
 
 import torch
 
-from .. import _native as nat
+from fasterkernels_amd import native as nat
 
 FP8_DTYPE = torch.float8_e4m3fn
 FP8_MAX = 448.0

@@ -53,7 +53,7 @@ except ImportError:  # pragma: no cover - transformers missing
     _native_eager = None
 
 if getattr(_native_eager, "_fsk_patch", False):  # imported after a patch was installed by hand
-    raise ImportError("fasterkernels_amd.hip.hf must be imported before eager_attention_forward is patched")
+    raise ImportError("fskernels.hip.hf must be imported before eager_attention_forward is patched")
 
 
 def native_eager_attention_forward(*args, **kwargs):

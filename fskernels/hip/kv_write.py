@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import torch
 
-from .. import _native as nat
+from fasterkernels_amd import native as nat
 from .decode import _on_gpu
 
 _SRC_DTYPES = (torch.float16, torch.bfloat16, torch.float32)

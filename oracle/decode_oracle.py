@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
 cpu_baseline leg may import this module, and only as the checker or the timed
-CPU baseline.  The product path (fasterkernels_amd) never imports it and has no
+CPU baseline.  The product path (fskernels, fasterkernels_amd) never imports it and has no
 CPU fallback.
 
 It restates, in plain numpy, what the reference computes on the decode path:

@@ -9,7 +9,7 @@ import subprocess
 import pytest
 import torch
 
-from fasterkernels_amd import _native as nat
+from fasterkernels_amd import native as nat
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(REPO, "include", "fsk_decode.h")
@@ -254,7 +254,7 @@ def test_timing_hook_without_gpu(lib):
 
 
 def test_python_wrappers_reject_host_tensors():
-    from fasterkernels_amd import paged_flash_decode, flash_decode_gqa_varlen
+    from fskernels.hip import paged_flash_decode, flash_decode_gqa_varlen
     q = torch.zeros(2, 32, 128, dtype=torch.float16)
     k = torch.zeros(4, 8, 16, 128, dtype=torch.float16)
     bt = torch.zeros(2, 2, dtype=torch.int32)

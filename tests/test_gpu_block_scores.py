@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from fasterkernels_amd import flash_decode_gqa_varlen, paged_flash_decode
+from fskernels.hip import flash_decode_gqa_varlen, paged_flash_decode
 from fasterkernels_amd import workloads as W
 from oracle import decode_oracle as O
 

@@ -12,9 +12,9 @@ import numpy as np
 import pytest
 import torch
 
-from fasterkernels_amd import _native as nat
+from fasterkernels_amd import native as nat
 from fasterkernels_amd import workloads as W
-from fasterkernels_amd.hip import decode as dec
+from fskernels.hip import decode as dec
 from oracle import decode_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -594,7 +594,7 @@ def test_dense_batch_above_one_wave():
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("skew", [0, 3, 20])
 def test_xcd_skew_splits(skew):
-    from fasterkernels_amd import _native as nat
+    from fasterkernels_amd import native as nat
     lens = [5000, 17000, 1, 9000, 12345, 20000, 700, 16000]  # total ~80K: 512+-token splits
     wl = W.make("C3", overrides=dict(B=len(lens), lens=("list", lens), sinks=True), seed=61)
     ref = oracle_for(wl)

@@ -1,4 +1,4 @@
-"""HIP-graph capture of decode steps (fasterkernels_amd.graph, .engine).
+"""HIP-graph capture of decode steps (fskernels.engine).
 
 Every replay is checked against the eager call on the same inputs (the
 kernels are deterministic for equal inputs, so bit-exact), with eager work
@@ -11,9 +11,10 @@ import numpy as np
 import pytest
 import torch
 
-from fasterkernels_amd import PagedKVCache, flash_decode_gqa_varlen, paged_flash_decode
-from fasterkernels_amd.graph import DecodeGraph, PagedDecodeStep
-from fasterkernels_amd.hip import decode as dec
+from fskernels.hip import flash_decode_gqa_varlen
+from fskernels.paged_attn import PagedKVCache, paged_flash_decode
+from fskernels.engine.hip_graph import DecodeGraph, PagedDecodeStep
+from fskernels.hip import decode as dec
 from oracle import decode_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -122,8 +123,8 @@ def test_hip_graph_runner_matches_fp32_attention_decoding():
     transformers = pytest.importorskip("transformers")
     import transformers.models.qwen3.modeling_qwen3 as qm
 
-    from fasterkernels_amd.engine import HIPGraphRunner
-    from fasterkernels_amd.hip import hf as H
+    from fskernels.engine import HIPGraphRunner
+    from fskernels.hip import hf as H
 
     cfg = transformers.Qwen3Config(vocab_size=256, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
                                    num_attention_heads=8, num_key_value_heads=2, head_dim=128,

@@ -1,4 +1,4 @@
-"""GPU parity of the HF attention patch (fasterkernels_amd.hip.hf).
+"""GPU parity of the HF attention patch (fskernels.hip.hf).
 
 Decode steps through the patch are compared with transformers' eager
 attention evaluated in float32 on the same inputs and mask (bar: atol = rtol
@@ -13,7 +13,7 @@ import torch
 
 transformers = pytest.importorskip("transformers")
 
-from fasterkernels_amd.hip import hf as H  # noqa: E402
+from fskernels.hip import hf as H  # noqa: E402
 from oracle import decode_oracle as O  # noqa: E402
 
 pytestmark = pytest.mark.gpu

@@ -10,8 +10,9 @@ import numpy as np
 import pytest
 import torch
 
-from fasterkernels_amd import PagedKVCache, paged_flash_decode, paged_kv_write
-from fasterkernels_amd.hip import decode as dec
+from fskernels.hip import paged_kv_write
+from fskernels.paged_attn import PagedKVCache, paged_flash_decode
+from fskernels.hip import decode as dec
 from oracle import decode_oracle as O
 
 pytestmark = pytest.mark.gpu

@@ -1,4 +1,4 @@
-"""HF attention patch (fasterkernels_amd.hip.hf) on the CPU: prefill calls go to
+"""HF attention patch (fskernels.hip.hf) on the CPU: prefill calls go to
 transformers' eager attention unchanged, decode steps refuse host tensors, and
 the patch helpers install and restore the module function."""
 import pytest
@@ -8,7 +8,7 @@ transformers = pytest.importorskip("transformers")
 
 import transformers.models.qwen3.modeling_qwen3 as qwen3_mod  # noqa: E402
 
-from fasterkernels_amd.hip import hf as H  # noqa: E402
+from fskernels.hip import hf as H  # noqa: E402
 
 
 class _Attn(torch.nn.Module):

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from fasterkernels_amd.paged_attn import PAGE_SIZE, PagedKVCache
+from fskernels.paged_attn import PAGE_SIZE, PagedKVCache
 from oracle import decode_oracle as O
 
 

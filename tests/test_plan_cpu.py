@@ -15,7 +15,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from fasterkernels_amd import _native as nat
+from fasterkernels_amd import native as nat
 
 CHUNK_MIN, CHUNK_MAX, SKEW_MIN = 128, 2048, 512
 

@@ -12,7 +12,7 @@ import ctypes
 import pytest
 import torch
 
-from fasterkernels_amd import _native as nat
+from fasterkernels_amd import native as nat
 from fasterkernels_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
