@@ -1,8 +1,12 @@
-"""Builds the gfx950 shared library ``libfsk_decode.so`` in-tree with hipcc.
+"""Builds the gfx950 shared library ``libfsk_decode.so`` and its torch-tensor
+binding ``_fsk_torch`` in-tree.
 
 Usage: ``python -m fasterkernels_amd.build`` (or ``__graft_entry__.build()``).
-The library is a plain C-ABI ``.so`` (see include/fsk_decode.h); Python loads
-it with ctypes, so no torch extension machinery is involved.
+The library is a plain C-ABI ``.so`` (see include/fsk_decode.h), built with
+hipcc for gfx950.  The binding (csrc/fsk_torch.cpp) is host-only C++ against
+torch's headers, linked to the library; the Python entry points call it (one
+C++ call per decode), and native.py's ctypes binding covers the rest of the
+C ABI (options, timing, debug entry points).
 """
 from __future__ import annotations
 
@@ -18,6 +22,8 @@ INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libfsk_decode.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = "gfx950"
+TORCH_SRC = os.path.join(PKG_DIR, "csrc", "fsk_torch.cpp")
+TORCH_EXT = "_fsk_torch"
 
 
 def hipcc() -> str:
@@ -37,8 +43,51 @@ def compile_flags() -> list[str]:
         # Packed-FP32 VALU ops are kept out of the generated code on purpose.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-fvisibility=hidden",
+        f"-Wl,-soname,{LIB_NAME}",
         f"-I{INCLUDE}",
     ]
+
+
+def torch_ext_path() -> str:
+    import sysconfig
+    return os.path.join(PKG_DIR, TORCH_EXT + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def torch_ext_command(out: str) -> list[str]:
+    """g++ line of the binding: torch's headers and pybind11, the C ABI header,
+    linked to libfsk_decode.so next to it (rpath $ORIGIN) and to torch."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension as ce
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if not cxx:
+        raise RuntimeError("a host C++ compiler (g++) is required to build the torch binding")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-fvisibility=hidden",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", f"-DTORCH_EXTENSION_NAME={TORCH_EXT}",
+           "-DTORCH_API_INCLUDE_EXTENSION_H", "-Wno-deprecated-declarations",
+           f"-I{INCLUDE}", f"-I{sysconfig.get_paths()['include']}"]
+    cmd += [f"-I{p}" for p in ce.include_paths()]
+    cmd += [TORCH_SRC, "-o", out, f"-L{PKG_DIR}", "-l:" + LIB_NAME, "-Wl,-rpath,$ORIGIN"]
+    for lib_dir in ce.library_paths():
+        cmd += [f"-L{lib_dir}", f"-Wl,-rpath,{lib_dir}"]
+    cmd += ["-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python"]
+    return cmd
+
+
+def build_torch_ext(verbose: bool = False) -> str:
+    """Compiles the torch binding (always; needs libfsk_decode.so built first)."""
+    out = torch_ext_path()
+    tmp = out + ".tmp"
+    cmd = torch_ext_command(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("building the torch binding failed:\n" + (res.stderr or "")[-4000:])
+    os.replace(tmp, out)
+    return out
 
 
 def build(verbose: bool = False) -> str:
@@ -56,6 +105,7 @@ def build(verbose: bool = False) -> str:
     if verbose and msgs:
         print("\n".join(msgs), file=sys.stderr)
     os.replace(tmp, LIB_PATH)
+    build_torch_ext(verbose)
     return LIB_PATH
 
 

@@ -157,6 +157,32 @@ def ptr(t) -> int | None:
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
+def raw_stream(index: int) -> int:
+    """Handle of torch's current stream on device ``index``."""
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
+
+
+_ext = None
+
+
+def ext():
+    """The torch binding (fasterkernels_amd._fsk_torch, built next to the
+    library by ``python -m fasterkernels_amd.build``): one C++ call per decode
+    or KV write.  Raises if it is not built; there is no other path."""
+    global _ext
+    if _ext is None:
+        load()  # the C library first: the binding links this same file
+        try:
+            from . import _fsk_torch
+        except ImportError as e:
+            raise RuntimeError("the torch binding of libfsk_decode.so is not built; run "
+                               f"`python -m fasterkernels_amd.build` ({e})") from None
+        _ext = _fsk_torch
+    return _ext
+
+
 def stream_handle(device: torch.device | int) -> int:
     """Handle of torch's current stream on ``device``."""
     index = device if isinstance(device, int) else device.index

@@ -2,10 +2,11 @@
 
 Each function keeps the name, positional signature, tensor layouts and return
 value of the reference entry point it replaces; new behaviour is only added
-through keyword-only arguments.  Every call validates its tensors, allocates
-the output and a split-KV workspace through torch's caching allocator, and
-launches the HIP kernels on torch's current stream (no host synchronisation,
-so the calls can be captured in a HIP graph).
+through keyword-only arguments.  Every call goes to the torch binding
+(fasterkernels_amd/csrc/fsk_torch.cpp) in one C++ call, which validates the
+tensors, allocates the output and a split-KV workspace through torch's
+caching allocator and launches the HIP kernels on torch's current stream (no
+host synchronisation, so the calls can be captured in a HIP graph).
 """
 from __future__ import annotations
 
@@ -71,12 +72,16 @@ def _on_gpu(t: torch.Tensor, name: str, device: torch.device | None = None) -> N
 
 def _inner_contig(t: torch.Tensor) -> torch.Tensor:
     """Innermost dim contiguous with 16-byte aligned rows, else a packed copy."""
-    if t.is_contiguous() and t.data_ptr() % 16 == 0 and (t.shape[-1] * t.element_size()) % 16 == 0:
-        return t
     es = t.element_size()
-    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(
-        (s * es) % 16 == 0 for s in t.stride()[:-1])
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((s * es) % 16 == 0 for s in t.stride()[:-1])
     return t if ok else t.contiguous()
+
+
+def _int32(t: torch.Tensor, name: str, device: torch.device) -> torch.Tensor:
+    _on_gpu(t, name, device)
+    if t.dtype is torch.int32 and t.is_contiguous():
+        return t
+    return t.to(torch.int32).contiguous()
 
 
 def _dtype_code(dt: torch.dtype, name: str) -> int:
@@ -86,38 +91,9 @@ def _dtype_code(dt: torch.dtype, name: str) -> int:
         raise NotImplementedError(f"{name}: unsupported dtype {dt}") from None
 
 
-def _int32(t: torch.Tensor, name: str, device: torch.device) -> torch.Tensor:
-    _on_gpu(t, name, device)
-    if t.dtype is torch.int32 and t.is_contiguous():
-        return t
-    if t.dtype != torch.int32:
-        t = t.to(torch.int32)
-    return t.contiguous()
-
-
-def _scale_ptr(s, device, name):
-    """Scales are device fp32 scalars (0-dim or 1-element tensors)."""
-    if s is None:
-        return None, None
-    if not isinstance(s, torch.Tensor):
-        s = torch.tensor(float(s), dtype=torch.float32, device=device)
-    _on_gpu(s, name, device)
-    if s.numel() != 1:
-        raise ValueError(f"{name} must hold a single per-tensor scale")
-    if s.dtype is not torch.float32:
-        s = s.to(torch.float32)
-    return s, s.data_ptr()  # one element: its address whatever the shape and strides
-
-
-def _sinks(s_aux, hq, device):
-    if s_aux is None:
-        return None
-    _on_gpu(s_aux, "s_aux", device)
-    if s_aux.numel() != hq:
-        raise ValueError(f"s_aux must have num_q_heads={hq} entries, got {tuple(s_aux.shape)}")
-    if s_aux.dtype is torch.float32 and s_aux.is_contiguous():
-        return s_aux
-    return s_aux.reshape(hq).to(torch.float32).contiguous()
+def _out_code(dt) -> int:
+    """Output dtype code for the binding (-1: the query's dtype)."""
+    return -1 if dt is None else _dtype_code(dt, "out_dtype")
 
 
 def _sink_mode(mode: str) -> int:
@@ -127,15 +103,40 @@ def _sink_mode(mode: str) -> int:
         raise ValueError(f"sink_mode must be 'exp' or 'linear', got {mode!r}") from None
 
 
-def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
-    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+_raw_stream = nat.raw_stream
 
 
-def _check_q(q: torch.Tensor):
+def _stream(q) -> int:
+    """torch's current HIP stream on q's device (0 for a host tensor, which
+    the binding then rejects)."""
+    if not isinstance(q, torch.Tensor):
+        raise TypeError("q must be a torch.Tensor")
+    index = q.get_device()
+    return _raw_stream(index) if index >= 0 else 0
+
+
+def _scale_tensor(s, like):
+    """Scales are device fp32 scalars; a Python number becomes one on like's device."""
+    if s is None or isinstance(s, torch.Tensor):
+        return s
+    return torch.tensor(float(s), dtype=torch.float32, device=like.device)
+
+
+def _scores_out(wanted, score_blocks, extent_tokens, q, odt):
+    """Block-score output [B, Hq, n] (n = score_blocks or ceil(extent / 128)), or None."""
+    if not wanted:
+        return None
     _on_gpu(q, "q")
     if q.dim() != 3:
         raise ValueError(f"q must be [batch, num_q_heads, head_dim], got {tuple(q.shape)}")
-    return _inner_contig(q)
+    n = int(score_blocks) if score_blocks is not None else max(1, -(-int(extent_tokens) // 128))
+    if n <= 0:
+        raise ValueError("score_blocks must be positive")
+    return torch.empty((q.shape[0], q.shape[1], n), dtype=odt or q.dtype, device=q.device)
+
+
+def _sm(sm_scale):
+    return None if sm_scale is None else float(sm_scale)
 
 
 # ---------------------------------------------------------------------------
@@ -163,58 +164,14 @@ def flash_decode_gqa_varlen(q, k_varlen, v_varlen, cu_seqlens_k, s_aux=None, *,
     (fskernels/tilelang/tilelang_gqa_decode.py:123-130); n = ``score_blocks``
     or enough blocks for total_tokens.
     """
-    q = _check_q(q)
-    dev = q.device
-    for t, n in ((k_varlen, "k_varlen"), (v_varlen, "v_varlen")):
-        _on_gpu(t, n, dev)
-        if t.dim() != 3:
-            raise ValueError(f"{n} must be [total_tokens, num_kv_heads, head_dim]")
-    k = _inner_contig(k_varlen)
-    v = _inner_contig(v_varlen)
-    B, Hq, D = q.shape
-    T, Hkv, Dk = k.shape
-    if v.shape != k.shape or Dk != D:
-        raise ValueError("k_varlen / v_varlen shapes disagree with q")
-    cu = _int32(cu_seqlens_k, "cu_seqlens_k", dev)
-    if cu.numel() != B + 1:
-        raise ValueError(f"cu_seqlens_k must have batch+1={B + 1} entries")
-    sinks = _sinks(s_aux, Hq, dev)
-    ks, ksp = _scale_ptr(k_scale, dev, "k_scale")
-    vs, vsp = _scale_ptr(v_scale, dev, "v_scale")
-    odt = out_dtype or q.dtype
-    out = torch.empty((B, Hq, D), dtype=odt, device=dev)
-    scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
-    nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_VARLEN, B, Hq, Hkv, D, T, 16, chunk_tokens, dev.index)
-    scores, nblk = _scores_out(return_block_scores, score_blocks, T, B, Hq, odt, dev)
-    if scores is not None:
-        nbytes += nat.score_workspace_bytes(B, Hq, nblk)
-    ws = _workspace(nbytes, dev)
-    lib = nat.load()
-    qs, kst, vst, os_ = q.stride(), k.stride(), v.stride(), out.stride()  # (one call each)
-    args = (q.data_ptr(), qs[0], qs[1],
-            k.data_ptr(), kst[0], kst[1],
-            v.data_ptr(), vst[0], vst[1],
-            cu.data_ptr(), T, nat.ptr(sinks), _sink_mode(sink_mode), ksp, vsp,
-            out.data_ptr(), os_[0], os_[1],
-            B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_varlen"),
-            _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens)
-    if scores is None:
-        st = nat.launch(dev.index, lib.fsk_decode_varlen, *args, nat.stream_handle(dev))
-    else:
-        st = nat.launch(dev.index, lib.fsk_decode_varlen_scores, *args, scores.data_ptr(), nblk,
-                        nat.stream_handle(dev))
-    nat.check(st)
+    scores = None
+    if return_block_scores:
+        _on_gpu(k_varlen, "k_varlen")
+        scores = _scores_out(True, score_blocks, k_varlen.shape[0], q, out_dtype)
+    out = nat.ext().varlen(q, k_varlen, v_varlen, cu_seqlens_k, s_aux, _scale_tensor(k_scale, q),
+                           _scale_tensor(v_scale, q), _out_code(out_dtype), _sink_mode(sink_mode), _sm(sm_scale),
+                           int(chunk_tokens), scores, _stream(q))
     return out if scores is None else (out, scores)
-
-
-def _scores_out(wanted, score_blocks, extent_tokens, B, Hq, odt, dev):
-    """Block-score output [B, Hq, n] (n = score_blocks or ceil(extent / 128)), or (None, 0)."""
-    if not wanted:
-        return None, 0
-    n = int(score_blocks) if score_blocks is not None else max(1, -(-int(extent_tokens) // 128))
-    if n <= 0:
-        raise ValueError("score_blocks must be positive")
-    return torch.empty((B, Hq, n), dtype=odt, device=dev), n
 
 
 # ---------------------------------------------------------------------------
@@ -223,49 +180,15 @@ def _scores_out(wanted, score_blocks, extent_tokens, B, Hq, odt, dev):
 def _dense(q, k_cache, v_cache, cache_lens, start_k_offsets, num_splits, *, q_scale=None,
            k_scale=None, v_scale=None, out_dtype=None, s_aux=None, sink_mode="exp",
            sm_scale=None, chunk_tokens=0):
-    q = _check_q(q)
-    dev = q.device
-    for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
-        _on_gpu(t, n, dev)
-        if t.dim() != 4:
-            raise ValueError(f"{n} must be [batch, num_kv_heads, max_seqlen, head_dim]")
-    k = _inner_contig(k_cache)
-    v = _inner_contig(v_cache)
-    B, Hq, D = q.shape
-    Bk, Hkv, S, Dk = k.shape
-    if v.shape != k.shape or Dk != D or Bk < B:
-        raise ValueError("k_cache / v_cache shapes disagree with q")
-    lens = _int32(cache_lens, "cache_lens", dev)
-    if lens.numel() < B:
-        raise ValueError("cache_lens must have one entry per sequence")
-    starts = None if start_k_offsets is None else _int32(start_k_offsets, "start_k_offsets", dev)
-    sinks = _sinks(s_aux, Hq, dev)
-    # (the scale tensors stay referenced until the launch: one made here from
-    # a float must not go back to the allocator before the kernel reads it)
-    qs, qsp = _scale_ptr(q_scale, dev, "scale_q")
-    ks, ksp = _scale_ptr(k_scale, dev, "scale_k")
-    vs, vsp = _scale_ptr(v_scale, dev, "scale_v")
-    odt = out_dtype or q.dtype
-    out = torch.empty((B, Hq, D), dtype=odt, device=dev)
-    scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
     if not chunk_tokens and num_splits and num_splits > 1:
+        _on_gpu(k_cache, "k_cache")
+        if k_cache.dim() != 4:
+            raise ValueError("k_cache must be [batch, num_kv_heads, max_seqlen, head_dim]")
+        S = k_cache.shape[2]
         chunk_tokens = max(32, -(-math.ceil(S / num_splits) // 32) * 32)
-    nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_DENSE, B, Hq, Hkv, D, S, 16, chunk_tokens, dev.index)
-    ws = _workspace(nbytes, dev)
-    lib = nat.load()
-    qst, kst, vst, os_ = q.stride(), k.stride(), v.stride(), out.stride()
-    st = nat.launch(
-        dev.index, lib.fsk_decode_dense,
-        q.data_ptr(), qst[0], qst[1],
-        k.data_ptr(), kst[0], kst[1], kst[2],
-        v.data_ptr(), vst[0], vst[1], vst[2], S,
-        lens.data_ptr(), nat.ptr(starts), nat.ptr(sinks), _sink_mode(sink_mode), qsp, ksp, vsp,
-        out.data_ptr(), os_[0], os_[1],
-        B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_cache"),
-        _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens,
-        nat.stream_handle(dev))
-    nat.check(st)
-    return out
+    return nat.ext().dense(q, k_cache, v_cache, cache_lens, start_k_offsets, s_aux, _scale_tensor(q_scale, q),
+                           _scale_tensor(k_scale, q), _scale_tensor(v_scale, q), _out_code(out_dtype),
+                           _sink_mode(sink_mode), _sm(sm_scale), int(chunk_tokens), _stream(q))
 
 
 def flash_decode_gqa_hf_dense_optimized(q, k_cache, v_cache, cache_lens, start_k_offsets=None,
@@ -319,59 +242,15 @@ def paged_flash_decode(q, k_pool, v_pool, block_table, seq_lens, page_size, *, s
     scales, which the reference kernel does not have, and the block scores of
     flash_decode_gqa_varlen (default width: the block table's token capacity).
     """
-    q = _check_q(q)
-    dev = q.device
-    for t, n in ((k_pool, "k_pool"), (v_pool, "v_pool")):
-        _on_gpu(t, n, dev)
-        if t.dim() != 4:
-            raise ValueError(f"{n} must be [num_pages, num_kv_heads, page_size, head_dim]")
-    k = _inner_contig(k_pool)
-    v = _inner_contig(v_pool)
-    B, Hq, D = q.shape
-    P, Hkv, PS, Dk = k.shape
-    if v.shape != k.shape or Dk != D:
-        raise ValueError("k_pool / v_pool shapes disagree with q")
-    if int(page_size) != PS:
-        raise ValueError(f"page_size={page_size} but the pools hold {PS}-token pages")
-    _on_gpu(block_table, "block_table", dev)
-    if block_table.dim() != 2 or block_table.shape[0] < B:
-        raise ValueError("block_table must be [batch, max_blocks]")
-    bt = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
-    bts = bt.stride()
-    if bts[1] != 1:
-        bt = bt.contiguous()
-        bts = bt.stride()
-    lens = _int32(seq_lens, "seq_lens", dev)
-    if lens.numel() < B:
-        raise ValueError("seq_lens must have one entry per sequence")
-    sinks = _sinks(s_aux, Hq, dev)
-    ks, ksp = _scale_ptr(k_scale, dev, "k_scale")
-    vs, vsp = _scale_ptr(v_scale, dev, "v_scale")
-    odt = out_dtype or q.dtype
-    out = torch.empty((B, Hq, D), dtype=odt, device=dev)
-    scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
-    max_blocks = bt.shape[1]
-    nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_PAGED, B, Hq, Hkv, D, max_blocks, PS, chunk_tokens, dev.index)
-    scores, nblk = _scores_out(return_block_scores, score_blocks, max_blocks * PS, B, Hq, odt, dev)
-    if scores is not None:
-        nbytes += nat.score_workspace_bytes(B, Hq, nblk)
-    ws = _workspace(nbytes, dev)
-    lib = nat.load()
-    qs, kst, vst, os_ = q.stride(), k.stride(), v.stride(), out.stride()
-    args = (q.data_ptr(), qs[0], qs[1],
-            k.data_ptr(), kst[0], kst[1], kst[2],
-            v.data_ptr(), vst[0], vst[1], vst[2],
-            bt.data_ptr(), bts[0], max_blocks, lens.data_ptr(), P, PS,
-            nat.ptr(sinks), _sink_mode(sink_mode), ksp, vsp,
-            out.data_ptr(), os_[0], os_[1],
-            B, Hq, Hkv, D, _dtype_code(q.dtype, "q"), _dtype_code(k.dtype, "k_pool"),
-            _dtype_code(odt, "out_dtype"), scale, ws.data_ptr(), nbytes, chunk_tokens)
-    if scores is None:
-        st = nat.launch(dev.index, lib.fsk_decode_paged, *args, nat.stream_handle(dev))
-    else:
-        st = nat.launch(dev.index, lib.fsk_decode_paged_scores, *args, scores.data_ptr(), nblk,
-                        nat.stream_handle(dev))
-    nat.check(st)
+    scores = None
+    if return_block_scores:
+        _on_gpu(block_table, "block_table")
+        if block_table.dim() != 2:
+            raise ValueError("block_table must be [batch, max_blocks]")
+        scores = _scores_out(True, score_blocks, block_table.shape[1] * int(page_size), q, out_dtype)
+    out = nat.ext().paged(q, k_pool, v_pool, block_table, seq_lens, int(page_size), s_aux,
+                          _scale_tensor(k_scale, q), _scale_tensor(v_scale, q), _out_code(out_dtype),
+                          _sink_mode(sink_mode), _sm(sm_scale), int(chunk_tokens), scores, _stream(q))
     return out if scores is None else (out, scores)
 
 

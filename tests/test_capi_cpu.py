@@ -316,3 +316,25 @@ def test_xcd_skew_option(lib):
     assert lib.fsk_set_option(b"xcd_skew", 51) == nat.FSK_ERR_INVALID
     assert lib.fsk_set_option(b"xcd_skew", 0) == nat.FSK_OK
     assert lib.fsk_set_option(b"xcd_skew", 3) == nat.FSK_OK
+
+
+def test_torch_binding_loads_with_the_library():
+    """The torch binding is built next to the library, links that same file
+    (one copy of the library's state: options, timing, last error) and
+    exposes the decode and write calls."""
+    import os
+    ext = nat.ext()
+    for name in ("paged", "varlen", "dense", "kv_write"):
+        assert callable(getattr(ext, name)), name
+    assert os.path.dirname(os.path.abspath(ext.__file__)) == os.path.dirname(nat.LIB_PATH)
+    maps = open("/proc/self/maps").read()
+    assert maps.count(os.path.realpath(nat.LIB_PATH)) >= 1
+    loaded = {line.split()[-1] for line in maps.splitlines() if line.endswith("libfsk_decode.so")}
+    assert loaded == {os.path.realpath(nat.LIB_PATH)}
+    # an option set through ctypes is seen by calls made through the binding
+    nat.set_option("chunk_tokens", 33 * 32)
+    try:
+        assert nat.load().fsk_workspace_bytes(1, 1, 8, 8, 128, 1 << 16, 16, 0) == \
+            nat.load().fsk_workspace_bytes(1, 1, 8, 8, 128, 1 << 16, 16, 33 * 32)
+    finally:
+        nat.set_option("chunk_tokens", 0)
