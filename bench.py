@@ -12,7 +12,11 @@ whole step (valid K+V bytes + Q + output + block-table entries + lengths) in
 GB/s; ``us_per_step`` and ``pct_of_peak`` (of 8 TB/s) are reported beside it.
 ``ms_per_step`` is the mean over the K timed steps (one wall-clock interval
 between synchronisations); ``us_per_step_median`` is the median over groups of
-10 steps of a following pass, from HIP events between the groups.
+10 steps of a following pass, from HIP events between the groups;
+``host_us_per_step`` is the host time spent issuing the timed steps (a step
+whose GPU work is shorter than this is host-bound).  ``--layers N`` makes a
+step N decode calls over N independent caches (``--with-write``: each after a
+one-token KV append), eager or, with ``--graph``, one captured graph.
 ``roofline`` is the split-KV partial kernel alone, timed with HIP events that
 its own dispatches stamp (hipExtLaunchKernel) on every call of a further
 pass of the same steps: the timing costs host time per call, so the step
@@ -59,6 +63,11 @@ def parse():
                     help="library option (fsk_set_option) set before the run, e.g. head_pairs=0; repeatable")
     ap.add_argument("--graph", action="store_true",
                     help="replay each decode step from a captured HIP graph (no per-step host work)")
+    ap.add_argument("--layers", type=int, default=1,
+                    help="decode calls per step, over that many independent caches (one decode step of an "
+                         "N-layer model); with --graph the whole step is one graph")
+    ap.add_argument("--with-write", action="store_true",
+                    help="with --layers: each layer first stores one new token per sequence (KV write kernel)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--traffic", default="",
@@ -356,22 +365,37 @@ def main():
         nat.set_option(name, int(value))
     base = W.make(args.config, gen_device=dev, device=dev)
     kv_bytes = base.k.numel() * base.k.element_size() * 2
+    L = max(1, args.layers)
     n_sets = args.sets or rotation_sets(kv_bytes)
+    n_sets = -(-max(n_sets, L) // L) * L     # whole groups of L layers
     # same lengths and page tables, independent K/V data
     sets = [base] + [W.make(args.config, gen_device=dev, device=dev, data_seed=base.meta["seed"] + 1000 * i)
                      for i in range(1, n_sets)]
     assert all(s.lens == base.lens for s in sets)
-    alg_bytes = base.algorithmic_bytes()
+    alg_bytes = base.algorithmic_bytes() * L
+    writes = [W.step_write(s, seed=5000 + i) for i, s in enumerate(sets)] if args.with_write else None
+    if args.with_write:
+        alg_bytes += sum(w.algorithmic_bytes() for w in writes[:L])
 
+    def layer_calls(g):
+        """The decode calls (and KV writes) of step group g, layer by layer."""
+        out = None
+        for j in range(g * L, g * L + L):
+            if writes is not None:
+                W.run_write(writes[j])
+            out = W.run(sets[j], chunk_tokens=args.chunk, block_scores=args.block_scores)
+        return out
+
+    n_groups = n_sets // L
     if args.graph:
         from fskernels.engine.hip_graph import DecodeGraph
-        graphs = [DecodeGraph(W.run, s, chunk_tokens=args.chunk, block_scores=args.block_scores) for s in sets]
+        graphs = [DecodeGraph(layer_calls, g) for g in range(n_groups)]
 
         def step(i):
-            return graphs[i % n_sets].replay()
+            return graphs[i % n_groups].replay()
     else:
         def step(i):
-            return W.run(sets[i % n_sets], chunk_tokens=args.chunk, block_scores=args.block_scores)
+            return layer_calls(i % n_groups)
 
     for i in range(args.warmup):
         step(i)
@@ -379,6 +403,7 @@ def main():
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(i)
+    issued = time.perf_counter() - t0   # host time to issue the steps (the host-bound limit)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     med_us = median_step_us(step, args.steps, args.steps)
@@ -401,11 +426,14 @@ def main():
         torch.cuda.synchronize()
         tot_ms = sum(a.elapsed_time(b) for a, b in evs)
         part_ms, calls = 0.0, len(evs)
+        tot_ms /= L  # per decode call of the replayed step
     else:
         # the partial and reduce kernels stamped by their own dispatches
+        # (decode calls only: the write kernels' stamps would join the triples)
         nat.enable_kernel_timing(KT_EVERY)
         for i in range(n_kt):
-            step(args.steps + i)
+            for j in range(L):
+                W.run(sets[(i * L + j) % n_sets], chunk_tokens=args.chunk, block_scores=args.block_scores)
         part_ms, tot_ms, calls = nat.kernel_timing()
         nat.enable_kernel_timing(0)
 
@@ -414,19 +442,22 @@ def main():
     part_avg_ms = part_ms / max(calls, 1)
     if args.graph:   # the replay (partial + reduce) is the timed unit
         part_avg_ms = tot_ms / max(calls, 1)
-    kern_gbs = alg_bytes / (part_avg_ms / 1e3) / 1e9 if part_avg_ms > 0 else None
+    call_bytes = base.algorithmic_bytes()
+    kern_gbs = call_bytes / (part_avg_ms / 1e3) / 1e9 if part_avg_ms > 0 else None
     traffic_file = args.traffic or os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                                 f"partial_kernel_{args.config}_traffic.md")
-    traffic = (None if (args.chunk or args.graph or args.block_scores or args.qk_engine != "mfma" or args.option)
-               else read_traffic(traffic_file))
+    traffic = (None if (args.chunk or args.graph or args.block_scores or args.qk_engine != "mfma" or args.option
+                        or L > 1) else read_traffic(traffic_file))
 
     out = {
-        "metric": METRIC if args.config == "M0" else (
-            f"µs/step + achieved HBM GB/s (% peak), {base.layout} GQA decode {args.config}"),
+        "metric": METRIC if (args.config == "M0" and L == 1) else (
+            f"µs/step + achieved HBM GB/s (% peak), {base.layout} GQA decode {args.config}"
+            + (f" x {L} layers" + (" with KV writes" if args.with_write else "") if L > 1 else "")),
         "value": round(gbs, 2),
         "unit": "GB/s",
         "us_per_step": round(ms_step * 1e3, 2),
         "us_per_step_median": round(med_us, 2),
+        "host_us_per_step": round(issued * 1e6 / args.steps, 2),
         "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
         "n_gpus": 1,
         "steps": args.steps,
@@ -446,6 +477,9 @@ def main():
             "qk_engine": args.qk_engine,
             "options": args.option,
             "block_scores": bool(args.block_scores),
+            "layers": L,
+            "with_write": bool(args.with_write),
+            "us_per_call": round(ms_step * 1e3 / L, 2),
         },
         "roofline": {
             "bound": "hbm",
@@ -454,7 +488,7 @@ def main():
             "unit": "GB/s",
             "frac": None if kern_gbs is None else round(kern_gbs / PEAK_HBM_GBS, 4),
             "traffic": traffic,
-            "kernel": ("partial_kernel + reduce_kernel (one graph replay)" if args.graph
+            "kernel": ("partial_kernel + reduce_kernel (graph replay time per decode call)" if args.graph
                        else "partial_kernel (split-KV partials)"),
             "kernel_avg_us": round(part_avg_ms * 1e3, 3),
             "partial_plus_reduce_avg_us": round(tot_ms / max(calls, 1) * 1e3, 3),

@@ -276,3 +276,31 @@ def run_write(wl: WriteWorkload) -> None:
     """One store of ``wl``'s rows through the HIP write entry point."""
     from fskernels.hip.kv_write import paged_kv_write
     paged_kv_write(wl.k, wl.v, wl.k_pool, wl.v_pool, wl.slots, k_scale=wl.k_scale, v_scale=wl.v_scale)
+
+
+def step_write(wl: Workload, *, seed: int = 0) -> WriteWorkload:
+    """One decode step's KV append for ``wl``: a new token for each of its
+    sequences (rows of q's dtype), stored into ``wl``'s own K/V (the pools
+    of a paged workload, at row 0 of free pages past the ones in use; the
+    last B rows of a varlen one, seen as a pool of one-row pages)."""
+    dev = wl.k.device
+    g = torch.Generator(device=dev).manual_seed(seed)
+    rows = wl.q.dtype if wl.q.dtype != torch.float8_e4m3fn else torch.bfloat16
+    k = torch.randn(wl.B, wl.Hkv, wl.D, device=dev, generator=g).to(rows)
+    v = torch.randn(wl.B, wl.Hkv, wl.D, device=dev, generator=g).to(rows)
+    if wl.layout == "paged":
+        used = torch.zeros(wl.k.shape[0], dtype=torch.bool, device=dev)
+        bt = wl.block_table.to(dev)
+        used[bt[bt >= 0].long()] = True
+        free = (~used).nonzero().flatten()
+        if free.numel() < wl.B:
+            raise ValueError("the pool has fewer free pages than sequences")
+        slots = free[:wl.B] * PAGE
+        kp, vp = wl.k, wl.v
+    else:
+        T = wl.k.shape[0]
+        slots = T - wl.B + torch.arange(wl.B, device=dev)
+        kp, vp = wl.k.unsqueeze(2), wl.v.unsqueeze(2)
+    return WriteWorkload(f"{wl.name}-append", k, v, slots.to(torch.int64), kp, vp, wl.k_scale, wl.v_scale,
+                         dict(src=str(rows).replace("torch.", ""), pool=str(wl.k.dtype).replace("torch.", ""),
+                              scaled=wl.k_scale is not None))
