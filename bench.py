@@ -74,6 +74,9 @@ def parse():
                     help="rocprof summary holding 'bytes_per_launch: N' for the measured kernel "
                          "(default: profiles/partial_kernel_<config>_traffic.md, or "
                          "kv_write_kernel_<config>_traffic.md for W0..W2, if committed)")
+    ap.add_argument("--wave-stamps", action="store_true",
+                    help="load the wave-stamp build and print the partial kernel's per-wave timeline "
+                         "(start-up, streaming, tail, dispatch) instead of the benchmark line")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration under rocprof)")
     return ap.parse_args()
@@ -337,8 +340,96 @@ def bench_write(args):
     print(json.dumps(out), flush=True)
 
 
+def wave_timeline(args):
+    """The partial kernel's per-wave timeline over several single calls
+    (after the warm-up): medians over calls of each stage, in µs from the
+    first wave's start (the s_memrealtime clock, 100 MHz).  The kernel's own
+    duration comes from its dispatch-stamped events on the same call."""
+    import numpy as np
+    import torch
+
+    from fasterkernels_amd import native as nat
+    lib = nat.use_stamped_library()
+    from fasterkernels_amd import workloads as W
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    for opt in args.option:
+        name, _, value = opt.partition("=")
+        nat.set_option(name, int(value))
+    base = W.make(args.config, gen_device=dev, device=dev)
+    n_sets = args.sets or rotation_sets(base.k.numel() * base.k.element_size() * 2)
+    sets = [base] + [W.make(args.config, gen_device=dev, device=dev, data_seed=base.meta["seed"] + 1000 * i)
+                     for i in range(1, n_sets)]
+    for i in range(args.warmup):
+        W.run(sets[i % n_sets], chunk_tokens=args.chunk)
+    calls = []
+    for r in range(max(5, min(args.steps, 50))):
+        for i in range(20):  # back-to-back calls before the recorded one, as in the timed steps
+            W.run(sets[(r + i) % n_sets], chunk_tokens=args.chunk)
+        torch.cuda.synchronize()
+        nat.check(lib.fsk_debug_clear_wave_stamps())
+        nat.enable_kernel_timing(1)
+        W.run(sets[r % n_sets], chunk_tokens=args.chunk)
+        part_ms, _, _ = nat.kernel_timing()
+        nat.enable_kernel_timing(0)
+        buf = np.zeros(4096 * 8, dtype=np.uint64)
+        nat.check(lib.fsk_debug_wave_stamps(buf.ctypes.data, 4096))
+        st = buf.reshape(4096, 8).astype(np.int64)
+        wg = np.arange(4096)[st[:, 0] > 0]   # workgroup ids of the waves that ran
+        st = st[st[:, 0] > 0]
+        t0 = st[:, 0].min()
+        us = lambda col: (st[:, col] - t0) * 0.01  # noqa: E731
+        work = st[:, 5] > 0
+        xcc = st[:, 6] & 0xF
+        # the first round of the grid (one workgroup per SIMD, dispatched first)
+        first_round = wg < 4 * torch.cuda.get_device_properties(dev).multi_processor_count
+
+        def med(x):
+            return float(np.median(x)) if len(x) else None
+        calls.append({
+            "kernel_us": part_ms * 1e3,
+            "first_round_first_tile_us": med(us(2)[work & first_round]),
+            "second_round_first_tile_us": med(us(2)[work & ~first_round]),
+            "first_round_end_median_us": med(us(3)[work & first_round]),
+            "second_round_end_median_us": med(us(3)[work & ~first_round]),
+            "one_segment_end_median_us": med(us(3)[work & (st[:, 5] == 1)]),
+            "two_segment_end_median_us": med(us(3)[work & (st[:, 5] == 2)]),
+            "two_segment_items": int((work & (st[:, 5] == 2)).sum()),
+            "waves": int(len(st)), "working_waves": int(work.sum()),
+            "start_spread_us": float(us(0).max()),
+            "plan_us_after_wave_start": float(np.median((st[:, 1] - st[:, 0]) * 0.01)),
+            "first_tile_us": float(np.median(us(2)[work])),
+            "first_tile_p90_us": float(np.percentile(us(2)[work], 90)),
+            "end_p10_us": float(np.percentile(us(3)[work], 10)),
+            "end_median_us": float(np.median(us(3)[work])),
+            "end_max_us": float(us(3)[work].max()),
+            "exit_max_us": float(us(4).max()),
+            "xcd_end_median_us": [float(np.median(us(3)[work & (xcc == x)])) if (work & (xcc == x)).any()
+                                  else None for x in range(8)],
+        })
+    med = {}
+    for k in calls[0]:
+        vals = [c[k] for c in calls if k != "xcd_end_median_us" and c[k] is not None]
+        if k != "xcd_end_median_us":
+            med[k] = round(float(np.median(vals)), 2) if vals else None
+    med["xcd_end_median_us"] = [round(float(np.median([c["xcd_end_median_us"][x] for c in calls
+                                                        if c["xcd_end_median_us"][x] is not None])), 2)
+                                for x in range(8)]
+    med["decomposition_us"] = {
+        "start_up": med["first_tile_us"],                                   # first wave start -> first tile (median)
+        "streaming": round(med["end_p10_us"] - med["first_tile_us"], 2),    # until the first 10 % of items end
+        "tail": round(med["exit_max_us"] - med["end_p10_us"], 2),           # until the last wave exits
+        "outside_waves": round(med["kernel_us"] - med["exit_max_us"], 2),   # dispatch before and after the waves
+    }
+    print(json.dumps({"wave_timeline": args.config, "calls": len(calls), "chunk_tokens": args.chunk or "auto",
+                      "options": args.option, "algorithmic_bytes": base.algorithmic_bytes(), **med}), flush=True)
+
+
 def main():
     args = parse()
+    if args.wave_stamps:
+        wave_timeline(args)
+        return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return

@@ -22,6 +22,7 @@ INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libfsk_decode.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = "gfx950"
+STAMPS_PATH = os.path.join(PKG_DIR, "libfsk_decode_stamps.so")  # -DFSK_WAVE_STAMPS (measurement build)
 TORCH_SRC = os.path.join(PKG_DIR, "csrc", "fsk_torch.cpp")
 TORCH_EXT = "_fsk_torch"
 
@@ -90,10 +91,9 @@ def build_torch_ext(verbose: bool = False) -> str:
     return out
 
 
-def build(verbose: bool = False) -> str:
-    """Compiles the library (always) and returns its path."""
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), *compile_flags(), SRC, "-o", tmp]
+def build_library(out: str, extra: list[str], verbose: bool) -> str:
+    tmp = out + ".tmp"
+    cmd = [hipcc(), *compile_flags(), *extra, SRC, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -104,7 +104,15 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
     if verbose and msgs:
         print("\n".join(msgs), file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, out)
+    return out
+
+
+def build(verbose: bool = False) -> str:
+    """Compiles the library, its wave-stamp twin and the torch binding
+    (always) and returns the library's path."""
+    build_library(LIB_PATH, [], verbose)
+    build_library(STAMPS_PATH, ["-DFSK_WAVE_STAMPS=1"], verbose)
     build_torch_ext(verbose)
     return LIB_PATH
 

@@ -45,6 +45,26 @@
 // hipGetSymbolAddress, once per device (see noalloc_scratch).
 static __device__ __align__(256) uint8_t scratch[FSK_NOALLOC_SCRATCH_BYTES];
 
+// Per-wave timeline of the partial kernel, in builds with FSK_WAVE_STAMPS
+// only (libfsk_decode_stamps.so; the normal library has none of this): lane
+// 0 of workgroup w < kStampWaves stores s_memrealtime (100 MHz) at its start
+// [0], when its plan is built [1], when the first tile of its first item is in
+// registers [2], after its last item's epilogue [3] and at its exit [4], plus
+// the number of segments it processed [5] and its XCC_ID [6].  Vector stores,
+// read back by fsk_debug_wave_stamps.
+#ifdef FSK_WAVE_STAMPS
+constexpr int kStampWaves = 4096;
+__device__ unsigned long long g_wave_stamps[kStampWaves * 8];
+#define FSK_STAMP_AT(slot, value)                                                         \
+  do {                                                                                     \
+    if (threadIdx.x == 0 && blockIdx.x < kStampWaves) g_wave_stamps[blockIdx.x * 8 + (slot)] = (value); \
+  } while (0)
+#define FSK_STAMP(slot) FSK_STAMP_AT(slot, __builtin_amdgcn_s_memrealtime())
+#else
+#define FSK_STAMP_AT(slot, value) do { } while (0)
+#define FSK_STAMP(slot) do { } while (0)
+#endif
+
 namespace {
 
 // ---------------------------------------------------------------------------
@@ -919,8 +939,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   const int g = lane >> 4;
   const int c = lane & 15;
 
+  FSK_STAMP(0);
+  FSK_STAMP_AT(6, (unsigned long long)__builtin_amdgcn_s_getreg((3 << 11) | 20));  // HW_REG_XCC_ID bits 3:0
+  FSK_STAMP_AT(2, 0ull);
+  FSK_STAMP_AT(3, 0ull);
   int lane_start, lane_len;  // start and length of sequence `lane` (B <= 64)
   const Split sp = build_plan<kLayout, kScores>(p, s_pre, s_flat, lane_start, lane_len);
+  FSK_STAMP(1);
+  int segments_done = 0;
   const int NH = p.n_items_h;
   const int64_t W = (int64_t)sp.n * NH;
   // Head pairs (varlen, head_dim 64, instantiated at D = 128): the token rows
@@ -1065,6 +1091,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
             const int sn = (s + kDepth - 1) % kDepth;
             issue_tile<D, kKV, kLayout>(tiles[sn], s_kstage + sn * 2 * TR::kHalfBytes, p, un, tn, g, c);
             wait_k_stage<TR::kLoads, kDepth>(kDepth - 1);
+            if (k == 0 && segments_done == 0) FSK_STAMP(2);
             if constexpr (kValu) {
               compute_tile_valu<D>(tiles[s], s_kstage + s * 2 * TR::kHalfBytes, sv, qv, sscale, g, c);
             } else {
@@ -1131,8 +1158,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
       }
       if (g == 0) *(f32x2*)(p.part_ml + 2 * idx) = f32x2{st.m_run, l_tot};
     }
+    ++segments_done;
+    FSK_STAMP(3);
     }  // segments of the chunk
   }
+  FSK_STAMP_AT(5, (unsigned long long)segments_done);
+  FSK_STAMP(4);
+  (void)segments_done;
 }
 
 // ---------------------------------------------------------------------------
@@ -2366,6 +2398,22 @@ int fsk_paged_gather(const void* pool, int64_t stride_p, int64_t stride_h, int64
   if (err != hipSuccess) return fail(FSK_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(err));
   return FSK_OK;
 }
+
+#ifdef FSK_WAVE_STAMPS
+int fsk_debug_wave_stamps(uint64_t* out, int waves) {
+  if (!out || waves < 0 || waves > kStampWaves) return fail(FSK_ERR_INVALID, "null pointer or waves out of range");
+  const hipError_t e = hipMemcpyFromSymbol(out, HIP_SYMBOL(g_wave_stamps), sizeof(uint64_t) * 8 * (size_t)waves);
+  if (e != hipSuccess) return fail(FSK_ERR_HIP, std::string("hipMemcpyFromSymbol: ") + hipGetErrorString(e));
+  return FSK_OK;
+}
+
+int fsk_debug_clear_wave_stamps(void) {
+  static const uint64_t zeros[kStampWaves * 8] = {0};
+  const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_wave_stamps), zeros, sizeof(zeros));
+  if (e != hipSuccess) return fail(FSK_ERR_HIP, std::string("hipMemcpyToSymbol: ") + hipGetErrorString(e));
+  return FSK_OK;
+}
+#endif
 
 int fsk_fp8_decode_table(uint16_t* out, void* stream) {
   if (!out || !aligned(out, 8)) return fail(FSK_ERR_INVALID, "null or unaligned pointer");

@@ -68,6 +68,12 @@ SIGNATURES = {
                                ctypes.POINTER(ctypes.c_int64)]),
 }
 
+# The two debug entry points of the wave-stamp build (libfsk_decode_stamps.so).
+STAMP_SIGNATURES = {
+    "fsk_debug_wave_stamps": (_I, [_P, _I]),
+    "fsk_debug_clear_wave_stamps": (_I, []),
+}
+
 _lock = threading.Lock()
 _lib = None
 
@@ -94,6 +100,24 @@ def load() -> ctypes.CDLL:
                 fn.argtypes = args
             _lib = lib
     return _lib
+
+
+def use_stamped_library() -> ctypes.CDLL:
+    """Loads the wave-stamp build instead of the normal library (before any
+    other use of this module in the process): the partial kernel then records
+    each wave's timeline (fsk_debug_wave_stamps).  Its soname is the normal
+    library's, so the torch binding imported afterwards binds to it."""
+    global LIB_PATH
+    if _lib is not None:
+        raise RuntimeError("the library is already loaded in this process")
+    from .build import STAMPS_PATH
+    LIB_PATH = STAMPS_PATH
+    lib = load()
+    for name, (res, args) in STAMP_SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
 
 
 def check(status: int) -> None:

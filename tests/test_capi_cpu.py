@@ -16,8 +16,12 @@ HEADER = os.path.join(REPO, "include", "fsk_decode.h")
 FAKE = 0x10000  # 64 KiB-aligned dummy address; never dereferenced on the host
 
 
-def header_functions():
+def header_functions(instrumented=False):
+    """Functions the header declares (those of the instrumented build, inside
+    #ifdef FSK_WAVE_STAMPS, only when ``instrumented``)."""
     text = open(HEADER).read()
+    if not instrumented:
+        text = re.sub(r"#ifdef FSK_WAVE_STAMPS.*?#endif", "", text, flags=re.S)
     return sorted(set(re.findall(r"FSK_API\s+[\w\s\*]+?\b(fsk_\w+)\s*\(", text)))
 
 
@@ -38,6 +42,21 @@ def test_exports_match_header(lib):
     assert sorted(nat.SIGNATURES) == declared
     for name in declared:
         assert getattr(lib, name) is not None
+
+
+def test_instrumented_library_exports():
+    """The wave-stamp build exports the same C ABI plus its two debug entry
+    points, under the same soname (so the torch binding binds to whichever
+    of the two libraries the process loaded first)."""
+    from fasterkernels_amd import build
+    if not os.path.exists(build.STAMPS_PATH):
+        pytest.skip("libfsk_decode_stamps.so not built")
+    out = subprocess.run(["nm", "-D", "--defined-only", build.STAMPS_PATH], capture_output=True, text=True).stdout
+    exported = sorted(set(re.findall(r"\bT (fsk_\w+)", out)))
+    assert exported == header_functions(instrumented=True)
+    assert set(exported) - set(header_functions()) == set(nat.STAMP_SIGNATURES)
+    dyn = subprocess.run(["readelf", "-d", build.STAMPS_PATH], capture_output=True, text=True).stdout
+    assert "SONAME" in dyn and "[libfsk_decode.so]" in dyn
 
 
 def test_version_and_options(lib):
