@@ -504,8 +504,10 @@ __device__ __forceinline__ int find_seq(const int32_t* pre, int B, int u) {
 //
 // Each wave software-pipelines its unit: the K/V loads of tile n+1 are in
 // flight while tile n is computed.  Paged units read their page ids once, into
-// a 128-entry window (two VGPRs, entry i in lane i % 64), so no block-table
-// load sits in front of a K/V load.
+// a 256-entry window (four VGPRs, entry i in lane i % 64), so no block-table
+// load sits in front of a K/V load.  (256 pages of 16 tokens allow 4096-token
+// chunks, so that long batches such as 32 x 8K or 64 x 6K tokens get one work
+// item per SIMD, not two: one wave per SIMD streams more evenly.)
 
 // First head_dim element of k-step i for k-group g (the same for Q and K).
 template <bool kKvFp8>
@@ -580,7 +582,7 @@ __device__ __forceinline__ void wait_k_stage(int later) {
 struct Unit {
   int b, kvh, start, len, t_begin, t_end;
   int p_first;     // paged: first logical page of the unit
-  int win0, win1;  // paged: physical page of logical page p_first + lane (+64)
+  int win0, win1, win2, win3;  // paged: physical page of logical page p_first + lane (+64, +128, +192)
 };
 
 template <int kLayout>
@@ -592,8 +594,11 @@ __device__ __forceinline__ HalfTile unit_half(const Params& p, const Unit& un, i
     if (h.rows > 0) {
       const int lp = t / p.page_size;
       off = t - lp * p.page_size;
-      const int idx = lp - un.p_first;  // 0 .. 127
-      page = idx < 64 ? __builtin_amdgcn_readlane(un.win0, idx) : __builtin_amdgcn_readlane(un.win1, idx - 64);
+      const int idx = lp - un.p_first;  // 0 .. 255
+      page = idx < 128 ? (idx < 64 ? __builtin_amdgcn_readlane(un.win0, idx)
+                                   : __builtin_amdgcn_readlane(un.win1, idx - 64))
+                       : (idx < 192 ? __builtin_amdgcn_readlane(un.win2, idx - 128)
+                                    : __builtin_amdgcn_readlane(un.win3, idx - 192));
     }
     h.k = p.k + (int64_t)page * p.k_s0 + un.kvh * p.k_sh + off * p.k_st;
     h.v = p.v + (int64_t)page * p.v_s0 + un.kvh * p.v_sh + off * p.v_st;
@@ -986,18 +991,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     const int u = uniform(s_pre[b]) + (jc - chunk_of(sp, fb));  // this segment's partial
     if (u >= p.u_max) continue;                          // (the host sizes u_max so this never holds)
     un.p_first = 0;
-    un.win0 = un.win1 = 0;
-    int win_raw0 = 0, win_raw1 = 0;
+    un.win0 = un.win1 = un.win2 = un.win3 = 0;
+    int win_raw0 = 0, win_raw1 = 0, win_raw2 = 0, win_raw3 = 0;
     if constexpr (kLayout == kPaged) {
       un.p_first = un.t_begin / p.page_size;
-      const int npg = (un.t_end - 1) / p.page_size - un.p_first + 1;  // <= 128 (chunk <= 2048)
+      const int npg = (un.t_end - 1) / p.page_size - un.p_first + 1;  // <= 256 (chunk <= 4096)
       const int32_t* row = p.block_table + (int64_t)un.b * p.bt_sb + un.p_first;
-      // Two range-checked loads (entries past npg read as 0) without
+      // Four range-checked loads (entries past npg read as 0) without
       // branches, so they and the Q loads below share one memory round trip;
       // the page ids are clamped to the pool once Q is in flight.
       const auto rw = make_rsrc(row, 4 * npg);
       win_raw0 = (int)buf_load<4>(rw, 4 * lane).w[0];
       win_raw1 = (int)buf_load<4>(rw, 4 * (lane + 64)).w[0];
+      win_raw2 = (int)buf_load<4>(rw, 4 * (lane + 128)).w[0];
+      win_raw3 = (int)buf_load<4>(rw, 4 * (lane + 192)).w[0];
     }
 
     // ---- Q^T operand: head c of this head block, zero for padding heads.
@@ -1047,6 +1054,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     if constexpr (kLayout == kPaged) {
       un.win0 = clampi(win_raw0, 0, p.num_pages - 1);
       un.win1 = clampi(win_raw1, 0, p.num_pages - 1);
+      un.win2 = clampi(win_raw2, 0, p.num_pages - 1);
+      un.win3 = clampi(win_raw3, 0, p.num_pages - 1);
     }
 
     SM st;
@@ -1638,7 +1647,7 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
 constexpr int kChunkMin = 128;   // smallest automatic split (tokens)
-constexpr int kChunkMax = 2048;  // largest split: 128 pages of 16 tokens per paged unit
+constexpr int kChunkMax = 4096;  // largest split: 256 pages of 16 tokens per paged unit (the page window)
 
 // Longest padded token stream a call can have (each sequence is padded to a
 // multiple of at most 128 tokens on the device).
@@ -1868,7 +1877,7 @@ int run_decode(const Common& c) {
   const bool pair =
       g_opt.head_pairs && pair_shape(c.layout, c.D, c.Hkv, G) && !c.scores && c.k_sh == 64 && c.v_sh == 64;
   if (c.layout == FSK_LAYOUT_PAGED && sp.chunk_max > kChunkMax)
-    return fail(FSK_ERR_UNSUPPORTED, "paged decode takes chunk_tokens <= 2048");
+    return fail(FSK_ERR_UNSUPPORTED, "paged decode takes chunk_tokens <= 4096");
   const int64_t u_max = sp.u_max;
   if (u_max >= ((int64_t)1 << 31) / (c.Hkv * (int64_t)n_hb)) return fail(FSK_ERR_UNSUPPORTED, "too many work units");
   const WsLayout wl = ws_layout(c.B, c.Hkv, G, c.D, u_max);

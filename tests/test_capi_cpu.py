@@ -144,7 +144,7 @@ def paged_args(**kw):
     (dict(ws=None), nat.FSK_ERR_WORKSPACE),
     (dict(wsb=1024), nat.FSK_ERR_WORKSPACE),
     (dict(chunk=48), nat.FSK_ERR_INVALID),
-    (dict(chunk=4096), nat.FSK_ERR_UNSUPPORTED),
+    (dict(chunk=4096 + 32), nat.FSK_ERR_UNSUPPORTED),         # above the 256-page window
     (dict(scale=float("nan")), nat.FSK_ERR_INVALID),
     # size arithmetic stays inside int64: strides, heads and batch are bounded
     (dict(q_sb=(1 << 62) + 8), nat.FSK_ERR_UNSUPPORTED),

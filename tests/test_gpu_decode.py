@@ -155,6 +155,16 @@ def test_paged_chunk_sizes(chunk):
     run_and_check(wl, chunk_tokens=chunk, what=f"chunk {chunk}")
 
 
+@pytest.mark.parametrize("name", ["C3", "C5"])
+@pytest.mark.parametrize("chunk", [2048, 2080, 4096])
+def test_paged_page_window_limits(name, chunk):
+    """Chunks of up to 4096 tokens: a unit reads up to 256 page ids (all four
+    window registers) of a shuffled pool, chunks start mid-sequence and span
+    sequence boundaries (f16, and e4m3 with sinks)."""
+    wl = W.make(name, overrides=dict(B=5, lens=("list", [4096, 8200, 5000, 33, 4097])), seed=5)
+    run_and_check(wl, chunk_tokens=chunk, what=f"{name} chunk {chunk}")
+
+
 @pytest.mark.parametrize("mode", ["exp", "linear"])
 @pytest.mark.parametrize("kv", ["f16", "bf16"])
 def test_paged_sinks(mode, kv):

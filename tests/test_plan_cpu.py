@@ -3,7 +3,7 @@
 fsk_debug_split runs the same split_geometry / chunk_lo / chunk_of / item_of
 code that every workgroup of the partial kernel runs, compiled for the host.
 The split policy arguments are the ones a decode call passes (automatic
-splits: chunk bounds 128..2048 tokens, 4 items per CU, the workspace capacity
+splits: chunk bounds 128..4096 tokens, 4 items per CU, the workspace capacity
 the host sizes; fixed splits: one chunk size, no XCD skew).  Checked: chunk
 sizes and alignment, contiguous coverage of the token stream, the token ->
 chunk map, room for every partial in the workspace, and that work items map
@@ -17,7 +17,7 @@ import pytest
 
 from fasterkernels_amd import native as nat
 
-CHUNK_MIN, CHUNK_MAX, SKEW_MIN = 128, 2048, 512
+CHUNK_MIN, CHUNK_MAX, SKEW_MIN = 128, 4096, 512
 
 
 def cdiv(a, b):

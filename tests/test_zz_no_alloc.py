@@ -70,7 +70,7 @@ def test_noalloc_refuses_shapes_beyond_the_scratch():
     """A batch whose workspace exceeds the scratch is refused with
     FSK_ERR_UNSUPPORTED and a message naming the limit; nothing is launched,
     so the output keeps its contents."""
-    B, Hq, Hkv, D, max_blocks = 128, 32, 8, 128, 2048
+    B, Hq, Hkv, D, max_blocks = 256, 32, 8, 128, 2048
     need = nat.workspace_bytes(nat.FSK_LAYOUT_PAGED, B, Hq, Hkv, D, max_blocks, 16, 0)
     assert need > SCRATCH_BYTES
     wl = W.make("M0", overrides=dict(B=B, lens=("fixed", 1), max_blocks=max_blocks), seed=43).to(DEV)
