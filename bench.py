@@ -386,6 +386,13 @@ def wave_timeline(args):
 
         def med(x):
             return float(np.median(x)) if len(x) else None
+        seg = st[:, 5]
+        ends = us(3)[work]
+        last = np.argsort(ends)[-16:]  # the 16 waves that end last
+        by_seg = {}
+        for k, sel in (("1", seg == 1), ("2", seg == 2), ("3", seg == 3), ("4plus", seg >= 4)):
+            by_seg[f"items_{k}_segments"] = int((work & sel).sum())
+            by_seg[f"end_median_us_{k}_segments"] = med(us(3)[work & sel])
         calls.append({
             "kernel_us": part_ms * 1e3,
             "first_round_first_tile_us": med(us(2)[work & first_round]),
@@ -404,6 +411,9 @@ def wave_timeline(args):
             "end_median_us": float(np.median(us(3)[work])),
             "end_max_us": float(us(3)[work].max()),
             "exit_max_us": float(us(4).max()),
+            "last16_mean_segments": float(seg[work][last].mean()),
+            "last16_first_tile_us": float(np.median(us(2)[work][last])),
+            **by_seg,
             "xcd_end_median_us": [float(np.median(us(3)[work & (xcc == x)])) if (work & (xcc == x)).any()
                                   else None for x in range(8)],
         })

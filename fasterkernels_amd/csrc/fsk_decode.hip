@@ -227,6 +227,7 @@ struct Params {
   int target_units;        // preferred number of sequence chunks per call
   int u_max;               // workspace capacity in units
   int xcd_skew;            // automatic split: long/short chunk pairs for even/odd XCDs, in % (0: equal)
+  int seg_tokens;          // stream tokens laid before each non-empty sequence (a multiple of 32)
   int32_t* plan;           // [B+1] unit prefix offsets
   float* part_ml;          // [u_max, Hkv, G, 2]
   float* part_acc;         // [u_max, Hkv, G, D]
@@ -299,7 +300,11 @@ __device__ __forceinline__ HalfTile half_tile(const Params& p, int b, int start,
 // stream positions [j*c, (j+1)*c) of one KV head.  A chunk that crosses
 // sequence boundaries is processed as one segment per sequence, and every
 // segment with valid tokens produces one fp32 partial, so all work items
-// carry the same number of tokens whatever the length distribution.
+// carry the same number of tokens whatever the length distribution.  Each
+// non-empty sequence is preceded in the stream by seg_tokens positions that
+// hold no tokens: a segment start costs its wave a few memory round trips
+// (partial store, page window and Q, first tiles), and an item that crosses
+// a sequence boundary carries that many fewer tokens in exchange.
 //
 // The chunk c is the larger of
 //   * stream / target (target = target_units, doubled while the chunk would
@@ -307,8 +312,9 @@ __device__ __forceinline__ HalfTile half_tile(const Params& p, int b, int start,
 //   * stream / (u_max - B - 1) (so every partial fits the workspace: a batch
 //     has at most n_chunks + B partials),
 // rounded to kAlign and clamped to [chunk_min, chunk_max]; the host sizes
-// u_max for chunk_max.  In LDS: flat[b] = stream offset of sequence b
-// (flat[B] = stream length), pre[b] = first partial of sequence b (pre[B] =
+// u_max for chunk_max.  In LDS: flat[b] = stream offset of sequence b's
+// region (its first token sits seg_tokens later; flat[B] = stream length),
+// pre[b] = first partial of sequence b (pre[B] =
 // total).  Workgroup 0 publishes pre for the reduce kernel.  Every workgroup
 // computes the same plan from the same lengths.  Returns the chunk count.
 // Chunk geometry.  The stream is cut into pairs of a long chunk (c_e tokens)
@@ -406,7 +412,7 @@ __host__ __device__ __forceinline__ Split split_geometry(uint32_t total, const S
 
 template <int kLayout, bool kScores>
 __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32_t* flat, int& start0_out,
-                                            int& len0_out) {
+                                            int& len0_out, int& seg_out) {
   constexpr int kAlign = kScores ? 128 : 32;
   const int lane = threadIdx.x;
   // Lengths of sequences lane, lane + 64, ...; the first block stays in a
@@ -431,13 +437,34 @@ __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32
   // arithmetic is unsigned 32-bit: the plan sits on every workgroup's
   // critical path, and 64-bit division is a long software sequence).
   uint32_t total = 0;
+  int nonempty = 0;   // sequences with tokens
+  int ref = -1;       // the first such sequence's length
+  bool varied = false;  // non-empty lengths differ
   for (int b0 = 0; b0 < p.B; b0 += kWave) {
-    const int padded = (length(b0, b0 + lane) + kAlign - 1) / kAlign * kAlign;
+    const int l = length(b0, b0 + lane);
+    const int padded = (l + kAlign - 1) / kAlign * kAlign;
     total += (uint32_t)__builtin_amdgcn_readlane(wave_incl_sum(padded), kWave - 1);
+    const uint64_t has = __ballot(l > 0);
+    nonempty += __builtin_popcountll(has);
+    if (ref < 0 && has) ref = __builtin_amdgcn_readlane(l, __builtin_ctzll(has));
+    varied = varied || __ballot(l > 0 && l != ref) != 0;
   }
   total = (uint32_t)uniform((int)total);
+  nonempty = uniform(nonempty);
   const SplitArgs sa{p.chunk_min, p.chunk_max, p.target_units, p.u_max, p.B, p.xcd_skew, p.n_items_h, kAlign};
   Split sp = split_geometry(total, sa);
+  // Lead-ins where sequence boundaries are common and fall anywhere: lengths
+  // that differ, at most 8 chunks per sequence.  Then many items hold a
+  // boundary, and the lead-ins balance them.  Equal lengths (whose chunks
+  // can line up with the sequences) and a few long sequences keep the plain
+  // split, where lead-ins measured slower.
+  int X = 0;
+  if (!kScores && p.seg_tokens > 0 && varied && sp.n <= 8 * nonempty) {
+    X = p.seg_tokens;
+    total += (uint32_t)(nonempty * X);
+    sp = split_geometry(total, sa);
+  }
+  seg_out = X;
   sp.c_e = uniform(sp.c_e);
   sp.c_o = uniform(sp.c_o);
   sp.pair = sp.c_e + sp.c_o;
@@ -448,10 +475,11 @@ __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32
   for (int b0 = 0; b0 < p.B; b0 += kWave) {
     const int b = b0 + lane;
     const int len = length(b0, b);
-    const int padded = (len + kAlign - 1) / kAlign * kAlign;
+    const int padded = (len + kAlign - 1) / kAlign * kAlign + (len > 0 ? X : 0);
     const int incl_f = wave_incl_sum(padded);
     const int fb = carry_f + incl_f - padded;
-    const int n = len > 0 ? chunk_of(sp, fb + len - 1) - chunk_of(sp, fb) + 1 : 0;
+    const int fs = fb + X;  // the sequence's first token in the stream
+    const int n = len > 0 ? chunk_of(sp, fs + len - 1) - chunk_of(sp, fs) + 1 : 0;
     const int incl_u = wave_incl_sum(n);
     if (b < p.B) {
       flat[b] = fb;
@@ -949,7 +977,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   FSK_STAMP_AT(2, 0ull);
   FSK_STAMP_AT(3, 0ull);
   int lane_start, lane_len;  // start and length of sequence `lane` (B <= 64)
-  const Split sp = build_plan<kLayout, kScores>(p, s_pre, s_flat, lane_start, lane_len);
+  int seg_x;  // empty stream positions before each sequence (see build_plan)
+  const Split sp = build_plan<kLayout, kScores>(p, s_pre, s_flat, lane_start, lane_len, seg_x);
   FSK_STAMP(1);
   int segments_done = 0;
   const int NH = p.n_items_h;
@@ -985,10 +1014,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
       un.start = uniform(un.start);
       un.len = uniform(un.len);
     }
-    un.t_begin = max(lo - fb, 0);
-    un.t_end = min(hi - fb, un.len);
-    if (un.t_end <= un.t_begin) continue;  // only padding of sequence b in this chunk
-    const int u = uniform(s_pre[b]) + (jc - chunk_of(sp, fb));  // this segment's partial
+    const int fs = fb + seg_x;  // sequence b's first token in the stream
+    un.t_begin = max(lo - fs, 0);
+    un.t_end = min(hi - fs, un.len);
+    if (un.t_end <= un.t_begin) continue;  // only padding (or the empty lead-in) of sequence b in this chunk
+    const int u = uniform(s_pre[b]) + (jc - chunk_of(sp, fs));  // this segment's partial
     if (u >= p.u_max) continue;                          // (the host sizes u_max so this never holds)
     un.p_first = 0;
     un.win0 = un.win1 = un.win2 = un.win3 = 0;
@@ -1569,6 +1599,7 @@ struct Options {
   int xcd_skew = 3;             // automatic split: extra share of the even XCDs, in % (see item_of)
   int qk_engine = 0;            // 0: QK and PV on the matrix cores; 1: the VALU tile (A/B measurement)
   int head_pairs = 1;           // varlen, head_dim 64: neighbouring KV heads as one 128-wide row (see pair_shape)
+  int seg_tokens = 96;          // lead-in per sequence in the work stream where boundaries are common (tokens)
 } g_opt;
 
 // Event triples of timed decode calls (the partial kernel's start and end and
@@ -1647,14 +1678,16 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
 constexpr int kChunkMin = 128;   // smallest automatic split (tokens)
+constexpr int kSegTokensMax = 256;  // largest lead-in per sequence (tokens)
 constexpr int kChunkMax = 4096;  // largest split: 256 pages of 16 tokens per paged unit (the page window)
 
 // Longest padded token stream a call can have (each sequence is padded to a
 // multiple of at most 128 tokens on the device).
 int64_t stream_bound(int layout, int B, int64_t kv_extent, int page_size) {
-  if (layout == FSK_LAYOUT_VARLEN) return kv_extent + 128 * (int64_t)B;
-  if (layout == FSK_LAYOUT_PAGED) return (int64_t)B * (kv_extent * page_size + 128);
-  return (int64_t)B * (kv_extent + 128);
+  constexpr int64_t kSlack = 128 + kSegTokensMax;  // padding and lead-in per sequence
+  if (layout == FSK_LAYOUT_VARLEN) return kv_extent + kSlack * (int64_t)B;
+  if (layout == FSK_LAYOUT_PAGED) return (int64_t)B * (kv_extent * page_size + kSlack);
+  return (int64_t)B * (kv_extent + kSlack);
 }
 
 // Partials a call can produce with split size `chunk` (host-side bound): the
@@ -1906,6 +1939,7 @@ int run_decode(const Common& c) {
   p.n_items_h = pair ? c.Hkv / 2 : c.Hkv * n_hb;
   p.chunk_min = sp.chunk_min; p.chunk_max = sp.chunk_max; p.target_units = sp.target_units;
   p.xcd_skew = sp.chunk_min == sp.chunk_max ? 0 : g_opt.xcd_skew;  // not with a fixed split
+  p.seg_tokens = g_opt.seg_tokens;
   p.u_max = (int)u_max;
   uint8_t* ws = (uint8_t*)c.ws;
   p.plan = (int32_t*)(ws + wl.plan_off);
@@ -2077,6 +2111,12 @@ int fsk_set_option(const char* name, int64_t value) {
   if (!strcmp(name, "chunk_tokens")) {
     if (value < 0 || value % 32 || value > (1 << 20)) return fail(FSK_ERR_INVALID, "chunk_tokens: 0 or a multiple of 32");
     g_opt.chunk_tokens = (int)value;
+    return FSK_OK;
+  }
+  if (!strcmp(name, "seg_tokens")) {
+    if (value < 0 || value > kSegTokensMax || value % 32)
+      return fail(FSK_ERR_INVALID, "seg_tokens: a multiple of 32 in [0, 256]");
+    g_opt.seg_tokens = (int)value;
     return FSK_OK;
   }
   if (!strcmp(name, "waves_per_cu")) {

@@ -72,6 +72,10 @@ def test_version_and_options(lib):
         assert lib.fsk_set_option(name, -1) == nat.FSK_ERR_INVALID
     assert lib.fsk_set_option(b"qk_engine", 0) == nat.FSK_OK
     assert lib.fsk_set_option(b"head_pairs", 1) == nat.FSK_OK
+    for bad in (-1, 33, 288):  # a multiple of 32 in [0, 256]
+        assert lib.fsk_set_option(b"seg_tokens", bad) == nat.FSK_ERR_INVALID
+    for ok in (0, 256, 96):
+        assert lib.fsk_set_option(b"seg_tokens", ok) == nat.FSK_OK
 
 
 def test_workspace_bytes(lib):

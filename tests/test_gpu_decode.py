@@ -155,6 +155,27 @@ def test_paged_chunk_sizes(chunk):
     run_and_check(wl, chunk_tokens=chunk, what=f"chunk {chunk}")
 
 
+@pytest.fixture
+def seg_tokens_option():
+    yield lambda v: nat.set_option("seg_tokens", v)
+    nat.set_option("seg_tokens", 96)
+
+
+@pytest.mark.parametrize("seg", [0, 32, 96, 256])
+@pytest.mark.parametrize("name,lens", [
+    ("C5", [4096, 8200, 5000, 33, 4097, 16, 700]),   # varied lengths: lead-ins in the plan
+    ("C5", [0, 900, 900, 900, 0, 900]),               # equal non-empty lengths: plain split
+    ("C1", [1, 2047, 0, 300, 129, 2048, 5, 1500]),    # varlen, short chunks
+])
+def test_sequence_lead_ins(seg_tokens_option, seg, name, lens):
+    """The work stream's lead-in before each sequence moves chunk boundaries,
+    not results: the oracle's output for every lead-in, including the
+    largest (256 tokens), on paged e4m3 with sinks and on varlen f16."""
+    seg_tokens_option(seg)
+    wl = W.make(name, overrides=dict(B=len(lens), lens=("list", lens)), seed=7)
+    run_and_check(wl, what=f"{name} seg_tokens {seg} lens {lens}")
+
+
 @pytest.mark.parametrize("name", ["C3", "C5"])
 @pytest.mark.parametrize("chunk", [2048, 2080, 4096])
 def test_paged_page_window_limits(name, chunk):
