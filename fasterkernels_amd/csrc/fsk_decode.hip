@@ -200,6 +200,15 @@ __device__ __forceinline__ Chunk<kBytes> buf_load(__amdgpu_buffer_rsrc_t r, int 
 __device__ __forceinline__ int clampi(int x, int lo, int hi) { return x < lo ? lo : (x > hi ? hi : x); }
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// Division by a divisor fixed per call, as a multiply and shift: m and s
+// from make_fastdiv on the host, exact for dividends below 2^31.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+__device__ __forceinline__ uint32_t fdiv(uint32_t x, FastDiv f) {
+  return (uint32_t)(((uint64_t)x * f.m) >> f.s);
+}
+
 // ---------------------------------------------------------------------------
 // Kernel parameters (passed by value)
 // ---------------------------------------------------------------------------
@@ -215,6 +224,7 @@ struct Params {
   const int32_t* block_table;
   int64_t bt_sb;           // elements
   int max_blocks, num_pages, page_size;
+  FastDiv page;            // divisor page_size (paged token -> page)
   int kv_extent;           // varlen: total rows; dense: S_max
   const float* q_scale;
   const float* k_scale;
@@ -620,13 +630,16 @@ __device__ __forceinline__ HalfTile unit_half(const Params& p, const Unit& un, i
   if constexpr (kLayout == kPaged) {
     int page = 0, off = 0;
     if (h.rows > 0) {
-      const int lp = t / p.page_size;
+      const int lp = (int)fdiv((uint32_t)t, p.page);
       off = t - lp * p.page_size;
       const int idx = lp - un.p_first;  // 0 .. 255
-      page = idx < 128 ? (idx < 64 ? __builtin_amdgcn_readlane(un.win0, idx)
-                                   : __builtin_amdgcn_readlane(un.win1, idx - 64))
-                       : (idx < 192 ? __builtin_amdgcn_readlane(un.win2, idx - 128)
-                                    : __builtin_amdgcn_readlane(un.win3, idx - 192));
+      // all four reads and two selects: no branches in the tile issue
+      const int w0 = __builtin_amdgcn_readlane(un.win0, idx & 63);
+      const int w1 = __builtin_amdgcn_readlane(un.win1, idx & 63);
+      const int w2 = __builtin_amdgcn_readlane(un.win2, idx & 63);
+      const int w3 = __builtin_amdgcn_readlane(un.win3, idx & 63);
+      const int lo = (idx & 64) ? w1 : w0, hi = (idx & 64) ? w3 : w2;
+      page = (idx & 128) ? hi : lo;
     }
     h.k = p.k + (int64_t)page * p.k_s0 + un.kvh * p.k_sh + off * p.k_st;
     h.v = p.v + (int64_t)page * p.v_s0 + un.kvh * p.v_sh + off * p.v_st;
@@ -1024,8 +1037,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     un.win0 = un.win1 = un.win2 = un.win3 = 0;
     int win_raw0 = 0, win_raw1 = 0, win_raw2 = 0, win_raw3 = 0;
     if constexpr (kLayout == kPaged) {
-      un.p_first = un.t_begin / p.page_size;
-      const int npg = (un.t_end - 1) / p.page_size - un.p_first + 1;  // <= 256 (chunk <= 4096)
+      un.p_first = (int)fdiv((uint32_t)un.t_begin, p.page);
+      const int npg = (int)fdiv((uint32_t)(un.t_end - 1), p.page) - un.p_first + 1;  // <= 256 (chunk <= 4096)
       const int32_t* row = p.block_table + (int64_t)un.b * p.bt_sb + un.p_first;
       // Four range-checked loads (entries past npg read as 0) without
       // branches, so they and the Q loads below share one memory round trip;
@@ -1399,13 +1412,6 @@ __global__ __launch_bounds__(64) void fp8_table_kernel(uint32_t* out) {
 // Division by a divisor d fixed per launch, for dividends below 2^31:
 // q = (x * m) >> s with s = 31 + ceil(log2 d), m = ceil(2^s / d).  The error
 // term (m d - 2^s) x / (d 2^s) stays below 1/d, so q == x / d exactly.
-struct FastDiv {
-  uint32_t d, m, s;
-};
-__device__ __forceinline__ uint32_t fdiv(uint32_t x, FastDiv f) {
-  return (uint32_t)(((uint64_t)x * f.m) >> f.s);
-}
-
 struct WriteParams {
   const uint8_t* src[2];               // K, V: [n, Hkv, D] rows
   int64_t s_st[2], s_sh[2];            // token / head strides, bytes
@@ -1897,6 +1903,13 @@ void launch_reduce(const ReduceParams& rp, int B, int o_dt, const Launch& s) {
   else launch(reduce_kernel<D, kF32>, grid, block, 0, s, rp);
 }
 
+FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while (((uint64_t)1 << l) < d) ++l;
+  const uint64_t two_s = (uint64_t)1 << (31 + l);
+  return FastDiv{d, (uint32_t)((two_s + d - 1) / d), 31 + l};
+}
+
 int run_decode(const Common& c) {
   int st = validate(c);
   if (st != FSK_OK) return st;
@@ -1931,6 +1944,7 @@ int run_decode(const Common& c) {
   p.lens = c.lens; p.starts = c.starts;
   p.block_table = c.bt; p.bt_sb = c.bt_sb; p.max_blocks = c.max_blocks;
   p.num_pages = c.num_pages; p.page_size = c.page_size > 0 ? c.page_size : 16;
+  p.page = make_fastdiv((uint32_t)p.page_size);
   p.kv_extent = (int)c.kv_extent;
   p.q_scale = c.q_scale; p.k_scale = c.k_scale; p.v_scale = c.v_scale;
   p.score_scale = c.sm_scale * kLog2e;
@@ -1994,12 +2008,6 @@ int run_decode(const Common& c) {
   return FSK_OK;
 }
 
-FastDiv make_fastdiv(uint32_t d) {
-  uint32_t l = 0;
-  while (((uint64_t)1 << l) < d) ++l;
-  const uint64_t two_s = (uint64_t)1 << (31 + l);
-  return FastDiv{d, (uint32_t)((two_s + d - 1) / d), 31 + l};
-}
 
 template <int kSrc, int kPool, bool kScaled>
 void launch_write(const WriteParams& p, dim3 grid, const Launch& s) {
