@@ -255,14 +255,16 @@ def test_write_kernels_load_whole_source_groups():
                           "--cuda-device-only", "-S", build.SRC, "-o", "-"],
                          capture_output=True, text=True, timeout=600)
     assert res.returncode == 0, res.stderr[-2000:]
+    # rows per thread per step (the kernel's unroll)
+    rows = int(re.search(r"#define FSK_WRITE_UNROLL (\d+)", open(build.SRC).read()).group(1))
     found = 0
     for m in re.finditer(r"\n(_ZN12_GLOBAL__N_115kv_write_kernelILi(\d)ELi(\d)ELb(\d)\w*):[^\n]*\n(.*?)s_endpgm",
                          res.stdout, re.S):
         src_dt, pool_dt, body = int(m.group(2)), int(m.group(3)), m.group(5)
         x4 = len(re.findall(r"global_load_dwordx4", body))
-        assert x4 == (8 if src_dt == nat.FSK_F32 else 4), (m.group(1), x4)   # 4 rows per thread
+        assert x4 == rows * (2 if src_dt == nat.FSK_F32 else 1), (m.group(1), x4, rows)
         if src_dt == nat.FSK_F16 and pool_dt != nat.FSK_F16:
-            assert len(re.findall(r"v_cvt_f32_f16", body)) == 32, m.group(1)
+            assert len(re.findall(r"v_cvt_f32_f16", body)) == 8 * rows, m.group(1)
         found += 1
     assert found == 12
 
