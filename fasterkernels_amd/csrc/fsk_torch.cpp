@@ -129,6 +129,19 @@ float softmax_scale(c10::optional<double> s, int64_t d) {
   return s ? (float)*s : (float)(1.0 / std::sqrt((double)d));
 }
 
+// Block-score output: the reduce kernel writes it as a contiguous
+// [batch, num_q_heads, n] array in the output dtype.
+bool score_tensor(const c10::optional<at::Tensor>& s, int64_t B, int64_t Hq, at::ScalarType odt,
+                  const c10::Device& dev) {
+  if (!s || !s->defined()) return false;
+  on_device(*s, "scores", dev);
+  if (s->dim() != 3 || s->size(0) != B || s->size(1) != Hq || s->size(2) < 1 || !s->is_contiguous() ||
+      s->scalar_type() != odt)
+    raise(FSK_ERR_INVALID, "scores must be a contiguous [" + std::to_string(B) + ", " + std::to_string(Hq) +
+                               ", n] tensor of the output dtype, got " + shape_str(*s));
+  return true;
+}
+
 at::Tensor workspace(int64_t nbytes, const at::Tensor& like) {
   if (nbytes < 0) check((int)nbytes);
   return at::empty({nbytes}, like.options().dtype(at::kByte));
@@ -169,7 +182,7 @@ at::Tensor paged(const at::Tensor& q_in, const at::Tensor& k_pool, const at::Ten
   int64_t nbytes = fsk_workspace_bytes(FSK_LAYOUT_PAGED, (int)B, (int)Hq, (int)Hkv, (int)D, max_blocks, (int)PS,
                                        (int)chunk_tokens);
   if (nbytes < 0) check((int)nbytes);
-  const bool with_scores = scores && scores->defined();
+  const bool with_scores = score_tensor(scores, B, Hq, out.scalar_type(), dev);
   if (with_scores) {
     const int64_t extra = fsk_score_workspace_bytes((int)B, (int)Hq, (int)scores->size(2));
     if (extra < 0) check((int)extra);
@@ -191,7 +204,6 @@ at::Tensor paged(const at::Tensor& q_in, const at::Tensor& k_pool, const at::Ten
                           (int)Hkv, (int)D, qd, kd, od, scl, ws.data_ptr(), nbytes, (int)chunk_tokens,
                           stream_ptr(stream));
   } else {
-    on_device(*scores, "scores", dev);
     st = fsk_decode_paged_scores(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
                                  k.stride(2), v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
                                  bt.data_ptr<int32_t>(), bt.stride(0), (int)max_blocks, lens.data_ptr<int32_t>(),
@@ -228,7 +240,7 @@ at::Tensor varlen(const at::Tensor& q_in, const at::Tensor& k_varlen, const at::
   const at::Tensor out = at::empty({B, Hq, D}, q.options().dtype(out_dtype(out_code, q)));
   int64_t nbytes = fsk_workspace_bytes(FSK_LAYOUT_VARLEN, (int)B, (int)Hq, (int)Hkv, (int)D, T, 16, (int)chunk_tokens);
   if (nbytes < 0) check((int)nbytes);
-  const bool with_scores = scores && scores->defined();
+  const bool with_scores = score_tensor(scores, B, Hq, out.scalar_type(), dev);
   if (with_scores) {
     const int64_t extra = fsk_score_workspace_bytes((int)B, (int)Hq, (int)scores->size(2));
     if (extra < 0) check((int)extra);
@@ -248,7 +260,6 @@ at::Tensor varlen(const at::Tensor& q_in, const at::Tensor& k_varlen, const at::
                            vsp, out.data_ptr(), out.stride(0), out.stride(1), (int)B, (int)Hq, (int)Hkv, (int)D, qd,
                            kd, od, scl, ws.data_ptr(), nbytes, (int)chunk_tokens, stream_ptr(stream));
   } else {
-    on_device(*scores, "scores", dev);
     st = fsk_decode_varlen_scores(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
                                   v.data_ptr(), v.stride(0), v.stride(1), cu.data_ptr<int32_t>(), T, sp,
                                   (int)sink_mode, ksp, vsp, out.data_ptr(), out.stride(0), out.stride(1), (int)B,

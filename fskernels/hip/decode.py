@@ -266,7 +266,11 @@ def paged_gather(pool, block_table, seq_lens):
     P, Hkv, PS, D = pool.shape
     bt = _int32(block_table, "block_table", dev)
     lens = _int32(seq_lens, "seq_lens", dev)
+    if bt.dim() != 2:
+        raise ValueError(f"block_table must be [batch, max_blocks], got {tuple(bt.shape)}")
     B, MB = bt.shape
+    if lens.numel() < B:
+        raise ValueError(f"seq_lens has {lens.numel()} entries for a batch of {B}")
     out = torch.empty((B, Hkv, MB * PS, D), dtype=pool.dtype, device=dev)
     lib = nat.load()
     st = nat.launch(dev.index, lib.fsk_paged_gather, pool.data_ptr(), pool.stride(0), pool.stride(1),

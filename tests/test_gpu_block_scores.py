@@ -98,3 +98,26 @@ def test_score_width_chunks_and_errors():
         flash_decode_gqa_varlen(*args, return_block_scores=True, chunk_tokens=96)
     with pytest.raises(ValueError):
         flash_decode_gqa_varlen(*args, return_block_scores=True, score_blocks=0)
+
+
+def test_binding_rejects_bad_score_tensors():
+    """The torch binding checks the score tensor it is handed (the reduce
+    kernel writes a contiguous [B, Hq, n] array in the output dtype)."""
+    from fasterkernels_amd import native as nat
+
+    q, k, v, cu, _ = varlen_case([300, 5], seed=6)
+    q, k, v, cu = q.to(DEV), k.to(DEV), v.to(DEV), cu.to(DEV)
+    stream = nat.raw_stream(q.get_device())
+    ext = nat.ext()
+    bad = [torch.empty(2, 32, dtype=torch.float16, device=DEV),                    # rank 2
+           torch.empty(3, 32, 4, dtype=torch.float16, device=DEV),                 # batch 3 for 2
+           torch.empty(2, 16, 4, dtype=torch.float16, device=DEV),                 # 16 heads for 32
+           torch.empty(2, 32, 4, dtype=torch.float32, device=DEV),                 # not the output dtype
+           torch.empty(2, 32, 8, dtype=torch.float16, device=DEV)[:, :, ::2]]      # not contiguous
+    for s in bad:
+        with pytest.raises(ValueError, match="scores must be"):
+            ext.varlen(q, k, v, cu, None, None, None, -1, 0, None, 0, s, stream)
+    good = torch.empty(2, 32, 4, dtype=torch.float16, device=DEV)
+    out = ext.varlen(q, k, v, cu, None, None, None, -1, 0, None, 0, good, stream)
+    torch.cuda.synchronize()
+    assert out.shape == (2, 32, 128) and torch.isfinite(good.float()).all()

@@ -534,6 +534,8 @@ def test_errors():
     with pytest.raises(ValueError):  # fp8 pools need scales
         k8 = wl.k.to(torch.float8_e4m3fn)
         dec.paged_flash_decode(wl.q, k8, k8, wl.block_table, wl.seq_lens, 16)
+    with pytest.raises(ValueError, match="seq_lens has 1 entries"):  # debug gather: one length per table row
+        dec.paged_gather(wl.k, wl.block_table, wl.seq_lens[:1])
 
 
 # ---------------------------------------------------------------------------
