@@ -341,10 +341,12 @@ def bench_write(args):
 
 
 def wave_timeline(args):
-    """The partial kernel's per-wave timeline over several single calls
-    (after the warm-up): medians over calls of each stage, in µs from the
-    first wave's start (the s_memrealtime clock, 100 MHz).  The kernel's own
-    duration comes from its dispatch-stamped events on the same call."""
+    """The partial kernel's per-wave timeline over several calls (after the
+    warm-up), each the last of 20 back-to-back calls: medians over calls of
+    each stage, in µs from the first wave's start (the s_memrealtime clock,
+    100 MHz), and how far the XCDs' median ends lie apart within a call.  The
+    kernel's own duration is the mean of its dispatch-stamped events over a
+    separate back-to-back pass."""
     import numpy as np
     import torch
 
@@ -362,16 +364,27 @@ def wave_timeline(args):
                      for i in range(1, n_sets)]
     for i in range(args.warmup):
         W.run(sets[i % n_sets], chunk_tokens=args.chunk)
+    n_rec = max(5, min(args.steps, 50))
+    # The kernel's own duration: dispatch-stamped events on every call of a
+    # separate back-to-back pass (its mean), as in the roofline pass.
+    nat.enable_kernel_timing(1)
+    for i in range(n_rec):
+        W.run(sets[i % n_sets], chunk_tokens=args.chunk)
+    part_ms, _, n_timed = nat.kernel_timing()
+    nat.enable_kernel_timing(0)
+    kernel_us = part_ms * 1e3 / max(n_timed, 1)
+    nat.check(lib.fsk_debug_clear_wave_stamps())
     calls = []
-    for r in range(max(5, min(args.steps, 50))):
-        for i in range(20):  # back-to-back calls before the recorded one, as in the timed steps
+    for r in range(n_rec):
+        # The recorded call is the last of 20 back-to-back calls, as in the
+        # timed steps: every wave of a call rewrites its own stamp slots, so
+        # the buffer read after the synchronisation holds that call's
+        # timeline.  (A call launched right after a synchronisation is not
+        # representative: its waves start together, but their first tiles
+        # arrive XCD by XCD, up to ~8 µs apart.)
+        for i in range(20):
             W.run(sets[(r + i) % n_sets], chunk_tokens=args.chunk)
         torch.cuda.synchronize()
-        nat.check(lib.fsk_debug_clear_wave_stamps())
-        nat.enable_kernel_timing(1)
-        W.run(sets[r % n_sets], chunk_tokens=args.chunk)
-        part_ms, _, _ = nat.kernel_timing()
-        nat.enable_kernel_timing(0)
         buf = np.zeros(4096 * 8, dtype=np.uint64)
         nat.check(lib.fsk_debug_wave_stamps(buf.ctypes.data, 4096))
         st = buf.reshape(4096, 8).astype(np.int64)
@@ -393,8 +406,10 @@ def wave_timeline(args):
         for k, sel in (("1", seg == 1), ("2", seg == 2), ("3", seg == 3), ("4plus", seg >= 4)):
             by_seg[f"items_{k}_segments"] = int((work & sel).sum())
             by_seg[f"end_median_us_{k}_segments"] = med(us(3)[work & sel])
+        xmed = [float(np.median(us(3)[work & (xcc == x)])) if (work & (xcc == x)).any() else None
+                for x in range(8)]
+        xvals = [v for v in xmed if v is not None]
         calls.append({
-            "kernel_us": part_ms * 1e3,
             "first_round_first_tile_us": med(us(2)[work & first_round]),
             "second_round_first_tile_us": med(us(2)[work & ~first_round]),
             "first_round_end_median_us": med(us(3)[work & first_round]),
@@ -414,10 +429,17 @@ def wave_timeline(args):
             "last16_mean_segments": float(seg[work][last].mean()),
             "last16_first_tile_us": float(np.median(us(2)[work][last])),
             **by_seg,
-            "xcd_end_median_us": [float(np.median(us(3)[work & (xcc == x)])) if (work & (xcc == x)).any()
-                                  else None for x in range(8)],
+            "xcd_end_median_us": xmed,
+            # per call: latest minus earliest XCD median end, and the last exit after their mean
+            "xcd_spread_us": float(max(xvals) - min(xvals)) if xvals else None,
+            "exit_after_xcd_mean_us": float(us(4).max() - np.mean(xvals)) if xvals else None,
         })
-    med = {}
+    med = {"kernel_us": round(kernel_us, 2)}
+    # which XCD ends late changes from call to call: the spread of each XCD's
+    # deviation from its call's mean (std over calls)
+    X = np.array([[v if v is not None else np.nan for v in c["xcd_end_median_us"]] for c in calls])
+    dev_ = X - np.nanmean(X, axis=1, keepdims=True)
+    med["xcd_deviation_std_us"] = [round(float(v), 2) for v in np.nanstd(dev_, axis=0)]
     for k in calls[0]:
         vals = [c[k] for c in calls if k != "xcd_end_median_us" and c[k] is not None]
         if k != "xcd_end_median_us":

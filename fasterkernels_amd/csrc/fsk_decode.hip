@@ -50,8 +50,9 @@ static __device__ __align__(256) uint8_t scratch[FSK_NOALLOC_SCRATCH_BYTES];
 // 0 of workgroup w < kStampWaves stores s_memrealtime (100 MHz) at its start
 // [0], when its plan is built [1], when the first tile of its first item is in
 // registers [2], after its last item's epilogue [3] and at its exit [4], plus
-// the number of segments it processed [5] and its XCC_ID [6].  Vector stores,
-// read back by fsk_debug_wave_stamps.
+// the number of segments it processed [5], its XCC_ID [6] and its HW_ID [7]
+// (wave slot, SIMD, CU, shader array and engine).  Vector stores, read back
+// by fsk_debug_wave_stamps.
 #ifdef FSK_WAVE_STAMPS
 constexpr int kStampWaves = 4096;
 __device__ unsigned long long g_wave_stamps[kStampWaves * 8];
@@ -987,6 +988,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
 
   FSK_STAMP(0);
   FSK_STAMP_AT(6, (unsigned long long)__builtin_amdgcn_s_getreg((3 << 11) | 20));  // HW_REG_XCC_ID bits 3:0
+  FSK_STAMP_AT(7, (unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 4));  // HW_REG_HW_ID, all 32 bits
   FSK_STAMP_AT(2, 0ull);
   FSK_STAMP_AT(3, 0ull);
   int lane_start, lane_len;  // start and length of sequence `lane` (B <= 64)
