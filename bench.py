@@ -28,7 +28,8 @@ load.
 
 Other workloads: ``--config C1..C5`` (decode configurations), ``--config M0b``
 (M0 with bf16 Q, KV and output), ``--config G1`` (varlen with sinks at head_dim
-64, Hq=64, Hkv=8), ``--config W0..W2`` (the KV write path: a
+64, Hq=64, Hkv=8), ``--config G2`` (paged at head_dim 256, 16384 tokens per
+sequence), ``--config W0..W2`` (the KV write path: a
 step is one store of a batch of new rows into scattered pages; ``roofline`` is
 the write kernel).  ``--graph`` replays each decode step from a captured HIP
 graph; ``--block-scores`` also computes the pooled 128-token block scores.
@@ -52,7 +53,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=300,
                     help="untimed steps first (the shader clock takes ~20 ms of load to settle)")
-    ap.add_argument("--config", default="M0", help="workload name (decode: M0, M0b, G1, C1..C5; KV write: W0..W2)")
+    ap.add_argument("--config", default="M0", help="workload name (decode: M0, M0b, G1, G2, C1..C5; KV write: W0..W2)")
     ap.add_argument("--sets", type=int, default=0, help="input sets to rotate (0: >= 4 and enough for > 1.1 GB)")
     ap.add_argument("--chunk", type=int, default=0, help="split size in tokens (0: library default)")
     ap.add_argument("--block-scores", action="store_true",

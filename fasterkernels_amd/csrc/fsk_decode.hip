@@ -1163,6 +1163,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
       for (int t = un.t_begin; t < un.t_end; t += 32) {
         issue_tile<D, kKV, kLayout>(ta, s_kstage, p, un, t, g, c);
         wait_k_stage<TR::kLoads, 1>(0);
+        if (t == un.t_begin && segments_done == 0) FSK_STAMP(2);
         if constexpr (kValu) {
           compute_tile_valu<D>(ta, s_kstage, sv, qv, sscale, g, c);
         } else {
@@ -1957,7 +1958,10 @@ int run_decode(const Common& c) {
   p.pair = pair ? 1 : 0;
   p.n_items_h = pair ? c.Hkv / 2 : c.Hkv * n_hb;
   p.chunk_min = sp.chunk_min; p.chunk_max = sp.chunk_max; p.target_units = sp.target_units;
-  p.xcd_skew = sp.chunk_min == sp.chunk_max ? 0 : g_opt.xcd_skew;  // not with a fixed split
+  // The skew is not applied to a fixed split, nor at head_dim 256: there the
+  // even and odd XCDs stream at the same rate (16-bit KV: partial kernel
+  // 3-4 % slower with it, paged and varlen; e4m3: no difference).
+  p.xcd_skew = (sp.chunk_min == sp.chunk_max || c.D > 128) ? 0 : g_opt.xcd_skew;
   p.seg_tokens = g_opt.seg_tokens;
   p.u_max = (int)u_max;
   uint8_t* ws = (uint8_t*)c.ws;

@@ -47,6 +47,10 @@ CONFIGS = {
     # B=4, Hq=64, Hkv=8, 65536 tokens each (the same 537 MB of K/V as M0)
     "G1": dict(layout="varlen", q="f16", kv="f16", out="f16", B=4, Hq=64, Hkv=8, D=64,
                lens=("fixed", 65536), sinks=True, seed=106),
+    # head_dim 256 (Gemma-style attention shapes): paged fp16, B=4, Hq=32,
+    # Hkv=8, 16384 tokens each (the same 537 MB of K/V as M0)
+    "G2": dict(layout="paged", q="f16", kv="f16", out="f16", B=4, Hq=32, Hkv=8, D=256,
+               lens=("fixed", 16384), sinks=False, seed=107),
 }
 
 DTYPES = {"f16": torch.float16, "bf16": torch.bfloat16, "e4m3": torch.float8_e4m3fn,
