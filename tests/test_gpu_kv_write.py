@@ -56,14 +56,14 @@ def source_values(n, hkv, d, src, gen, spread=40.0):
     special = torch.tensor([0.0, -0.0, 448.0, -448.0, 464.0, -464.0, 470.0, 1e5, -1e5, float("inf"),
                             float("-inf"), float("nan"), -float("nan"), 65504.0, 65520.0, 1e-7, -3e-8])
     idx = torch.randperm(flat.numel(), generator=gen)[:4 * special.numel()]
-    flat[idx] = special.repeat(4)
+    flat[idx] = special.repeat(4)[:idx.numel()]   # (small tensors take the first ones)
     if src == "f32":  # f16 and bf16 rounding ties
         u = torch.randint(0, 1 << 15, (512,), generator=gen, dtype=torch.int32)
         ties = ((u << 16) | 0x8000).view(torch.float32)
         h = torch.randint(0, 0x7C00, (512,), generator=gen, dtype=torch.int32).to(torch.int16)
         ties16 = (h.view(torch.float16).float().view(torch.int32) | 0x1000).view(torch.float32)
         idx = torch.randperm(flat.numel(), generator=gen)[:1024]
-        flat[idx] = torch.cat([ties, ties16])
+        flat[idx] = torch.cat([ties, ties16])[:idx.numel()]
     return x.to(SRC[src])
 
 
