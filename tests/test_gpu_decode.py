@@ -6,7 +6,6 @@ oracle plus half an ulp of the output dtype (the final cast's own rounding);
 fp8-KV outputs within atol = 1e-2; page gathers and the e4m3 decode table
 bit-exact.
 """
-import math
 
 import numpy as np
 import pytest

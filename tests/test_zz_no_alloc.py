@@ -7,7 +7,6 @@ different data, check that nothing of the first call's scratch contents leaks
 into the second; a shape whose workspace exceeds the scratch is refused
 before any launch.
 """
-import ctypes
 
 import pytest
 import torch
