@@ -386,9 +386,9 @@ def wave_timeline(args):
         for i in range(20):
             W.run(sets[(r + i) % n_sets], chunk_tokens=args.chunk)
         torch.cuda.synchronize()
-        buf = np.zeros(4096 * 8, dtype=np.uint64)
+        buf = np.zeros(4096 * 16, dtype=np.uint64)
         nat.check(lib.fsk_debug_wave_stamps(buf.ctypes.data, 4096))
-        st = buf.reshape(4096, 8).astype(np.int64)
+        st = buf.reshape(4096, 16).astype(np.int64)
         wg = np.arange(4096)[st[:, 0] > 0]   # workgroup ids of the waves that ran
         st = st[st[:, 0] > 0]
         t0 = st[:, 0].min()
@@ -421,6 +421,10 @@ def wave_timeline(args):
             "waves": int(len(st)), "working_waves": int(work.sum()),
             "start_spread_us": float(us(0).max()),
             "plan_us_after_wave_start": float(np.median((st[:, 1] - st[:, 0]) * 0.01)),
+            # paged: first item's set-up after the plan, its page window + Q round trip, then its first tiles
+            "item_setup_us": med(((st[:, 8] - st[:, 1]) * 0.01)[work & (st[:, 8] > 0)]),
+            "window_round_trip_us": med(((st[:, 9] - st[:, 8]) * 0.01)[work & (st[:, 9] > 0)]),
+            "first_tile_after_window_us": med(((st[:, 2] - st[:, 9]) * 0.01)[work & (st[:, 9] > 0) & (st[:, 2] > 0)]),
             "first_tile_us": float(np.median(us(2)[work])),
             "first_tile_p90_us": float(np.percentile(us(2)[work], 90)),
             "end_p10_us": float(np.percentile(us(3)[work], 10)),

@@ -51,14 +51,16 @@ static __device__ __align__(256) uint8_t scratch[FSK_NOALLOC_SCRATCH_BYTES];
 // [0], when its plan is built [1], when the first tile of its first item is in
 // registers [2], after its last item's epilogue [3] and at its exit [4], plus
 // the number of segments it processed [5], its XCC_ID [6] and its HW_ID [7]
-// (wave slot, SIMD, CU, shader array and engine).  Vector stores, read back
-// by fsk_debug_wave_stamps.
+// (wave slot, SIMD, CU, shader array and engine), and for its first item
+// (paged units) when the page window and Q loads are issued [8] and when
+// they have arrived [9].  Vector stores, read back by fsk_debug_wave_stamps.
 #ifdef FSK_WAVE_STAMPS
 constexpr int kStampWaves = 4096;
-__device__ unsigned long long g_wave_stamps[kStampWaves * 8];
+constexpr int kStampSlots = 16;
+__device__ unsigned long long g_wave_stamps[kStampWaves * kStampSlots];
 #define FSK_STAMP_AT(slot, value)                                                         \
   do {                                                                                     \
-    if (threadIdx.x == 0 && blockIdx.x < kStampWaves) g_wave_stamps[blockIdx.x * 8 + (slot)] = (value); \
+    if (threadIdx.x == 0 && blockIdx.x < kStampWaves) g_wave_stamps[blockIdx.x * kStampSlots + (slot)] = (value); \
   } while (0)
 #define FSK_STAMP(slot) FSK_STAMP_AT(slot, __builtin_amdgcn_s_memrealtime())
 #else
@@ -206,7 +208,7 @@ __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirs
 struct FastDiv {
   uint32_t d, m, s;
 };
-__device__ __forceinline__ uint32_t fdiv(uint32_t x, FastDiv f) {
+__host__ __device__ __forceinline__ uint32_t fdiv(uint32_t x, FastDiv f) {
   return (uint32_t)(((uint64_t)x * f.m) >> f.s);
 }
 
@@ -233,6 +235,7 @@ struct Params {
   float score_scale;       // sm_scale * log2(e)
   int B, Hkv, G, n_hb;
   int n_items_h;           // head slots per chunk: Hkv * n_hb, or Hkv / 2 with pair
+  FastDiv nh_div;          // divisor n_items_h
   int pair;                // varlen, head_dim 64: a wave takes KV heads 2i and 2i+1 as one 128-wide row
   int chunk_min, chunk_max;  // split size bounds in tokens (multiples of 32)
   int target_units;        // preferred number of sequence chunks per call
@@ -351,17 +354,20 @@ __host__ __device__ __forceinline__ int chunk_len(const Split& sp, int j) { retu
 // with a skew the long (even) chunks go to the even XCDs: item w = 8 m + x
 // takes pair index P = 4 m + x / 2 of its parity class, chunk 2 (P / NH) +
 // (x & 1), head slot P mod NH.  (A bijection when n is even and n NH is a
-// multiple of 8, which the plan ensures before setting `paired`.)
-__host__ __device__ __forceinline__ void item_of(const Split& sp, int64_t w, int NH, int& jc, int& hh) {
+// multiple of 8, which the plan ensures before setting `paired`.)  nh
+// divides by NH; w < 2^31 (the host bounds the item count), so 32-bit
+// arithmetic and the multiply-shift division are exact.
+__host__ __device__ __forceinline__ void item_of(const Split& sp, uint32_t w, FastDiv nh, int& jc, int& hh) {
   if (sp.paired) {
-    const int x = (int)(w & 7);
-    const int64_t P = (w >> 3) * 4 + (x >> 1);
-    const int64_t q = P / NH;
-    jc = (int)(2 * q) + (x & 1);
-    hh = (int)(P - q * NH);
+    const uint32_t x = w & 7;
+    const uint32_t P = (w >> 3) * 4 + (x >> 1);
+    const uint32_t q = fdiv(P, nh);
+    jc = (int)(2 * q + (x & 1));
+    hh = (int)(P - q * nh.d);
   } else {
-    jc = (int)(w / NH);
-    hh = (int)(w - (int64_t)jc * NH);
+    const uint32_t q = fdiv(w, nh);
+    jc = (int)q;
+    hh = (int)(w - q * nh.d);
   }
 }
 
@@ -423,7 +429,7 @@ __host__ __device__ __forceinline__ Split split_geometry(uint32_t total, const S
 
 template <int kLayout, bool kScores>
 __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32_t* flat, int& start0_out,
-                                            int& len0_out, int& seg_out) {
+                                            int& len0_out, int& seg_out, int& flat0_out, int& pre0_out) {
   constexpr int kAlign = kScores ? 128 : 32;
   const int lane = threadIdx.x;
   // Lengths of sequences lane, lane + 64, ...; the first block stays in a
@@ -492,9 +498,14 @@ __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32
     const int fs = fb + X;  // the sequence's first token in the stream
     const int n = len > 0 ? chunk_of(sp, fs + len - 1) - chunk_of(sp, fs) + 1 : 0;
     const int incl_u = wave_incl_sum(n);
+    const int pb = min(carry_u + incl_u - n, p.u_max);  // the cap never binds with the host's u_max
     if (b < p.B) {
       flat[b] = fb;
-      pre[b] = min(carry_u + incl_u - n, p.u_max);  // the cap never binds with the host's u_max
+      pre[b] = pb;
+    }
+    if (b0 == 0) {  // lane b's entries (lanes past B hold flat[B] and pre[B])
+      flat0_out = fb;
+      pre0_out = pb;
     }
     if constexpr (kScores)
       if (blockIdx.x == 0 && b < p.B) p.lens_out[b] = len;
@@ -992,12 +1003,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   FSK_STAMP_AT(2, 0ull);
   FSK_STAMP_AT(3, 0ull);
   int lane_start, lane_len;  // start and length of sequence `lane` (B <= 64)
+  int lane_flat, lane_pre;   // flat[lane] and pre[lane] of the plan (B <= 64)
   int seg_x;  // empty stream positions before each sequence (see build_plan)
-  const Split sp = build_plan<kLayout, kScores>(p, s_pre, s_flat, lane_start, lane_len, seg_x);
+  const Split sp = build_plan<kLayout, kScores>(p, s_pre, s_flat, lane_start, lane_len, seg_x, lane_flat, lane_pre);
   FSK_STAMP(1);
   int segments_done = 0;
   const int NH = p.n_items_h;
-  const int64_t W = (int64_t)sp.n * NH;
+  const int W = sp.n * NH;  // < 2^31: the host bounds the workspace's units times NH
+  // Plan tables: from the lanes' registers when B <= 64 (no LDS round trips
+  // on the way to a unit's first loads), else from LDS.
+  const bool small_b = p.B <= kWave;
+  auto flat_at = [&](int b) { return small_b ? __builtin_amdgcn_readlane(lane_flat, b) : uniform(s_flat[b]); };
+  auto pre_at = [&](int b) { return small_b ? __builtin_amdgcn_readlane(lane_pre, b) : uniform(s_pre[b]); };
   // Head pairs (varlen, head_dim 64, instantiated at D = 128): the token rows
   // of KV heads 2i and 2i+1 are 128-byte neighbours in [T, Hkv, 64], read as
   // one 256-byte row.  Columns 0..G-1 are head 2i's query heads with Q zero
@@ -1009,14 +1026,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   const float v_scale = kKvFp8 ? p.v_scale[0] : 1.0f;
   const float sscale = p.score_scale * k_scale;
 
-  for (int64_t w = blockIdx.x; w < W; w += gridDim.x) {
+  for (int w = blockIdx.x; w < W; w += gridDim.x) {
     int jc, hh;
-    item_of(sp, w, NH, jc, hh);
-    const int kvh = hh / p.n_hb;  // (with pair: the pair index, n_hb = 1)
+    item_of(sp, (uint32_t)w, p.nh_div, jc, hh);
+    const int kvh = p.n_hb == 1 ? hh : hh / p.n_hb;  // (with pair: the pair index, n_hb = 1)
     const int hb = hh - kvh * p.n_hb;
     const int lo = chunk_lo(sp, jc), hi = lo + chunk_len(sp, jc);  // stream range of this chunk
-    for (int b = uniform(find_seq(s_flat, p.B, lo)); b < p.B; ++b) {
-    const int fb = uniform(s_flat[b]);
+    // the last sequence whose region starts at or before lo (flat is nondecreasing, flat[0] = 0)
+    const int b_first = small_b ? __builtin_popcountll(__ballot(lane < p.B && lane_flat <= lo)) - 1
+                                : find_seq(s_flat, p.B, lo);
+    for (int b = uniform(b_first); b < p.B; ++b) {
+    const int fb = flat_at(b);
     if (fb >= hi) break;
     Unit un;
     un.b = b;
@@ -1033,11 +1053,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     un.t_begin = max(lo - fs, 0);
     un.t_end = min(hi - fs, un.len);
     if (un.t_end <= un.t_begin) continue;  // only padding (or the empty lead-in) of sequence b in this chunk
-    const int u = uniform(s_pre[b]) + (jc - chunk_of(sp, fs));  // this segment's partial
+    const int u = pre_at(b) + (jc - chunk_of(sp, fs));  // this segment's partial
     if (u >= p.u_max) continue;                          // (the host sizes u_max so this never holds)
     un.p_first = 0;
     un.win0 = un.win1 = un.win2 = un.win3 = 0;
     int win_raw0 = 0, win_raw1 = 0, win_raw2 = 0, win_raw3 = 0;
+    if (segments_done == 0) FSK_STAMP(8);
     if constexpr (kLayout == kPaged) {
       un.p_first = (int)fdiv((uint32_t)un.t_begin, p.page);
       const int npg = (int)fdiv((uint32_t)(un.t_end - 1), p.page) - un.p_first + 1;  // <= 256 (chunk <= 4096)
@@ -1101,6 +1122,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
       un.win1 = clampi(win_raw1, 0, p.num_pages - 1);
       un.win2 = clampi(win_raw2, 0, p.num_pages - 1);
       un.win3 = clampi(win_raw3, 0, p.num_pages - 1);
+#ifdef FSK_WAVE_STAMPS
+      // (the first tile's issue waits for the window anyway; Q shares its round trip)
+      if (segments_done == 0) {
+        __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
+        FSK_STAMP(9);
+      }
+#endif
     }
 
     SM st;
@@ -1957,6 +1985,7 @@ int run_decode(const Common& c) {
   p.B = c.B; p.Hkv = c.Hkv; p.G = G; p.n_hb = n_hb;
   p.pair = pair ? 1 : 0;
   p.n_items_h = pair ? c.Hkv / 2 : c.Hkv * n_hb;
+  p.nh_div = make_fastdiv((uint32_t)p.n_items_h);
   p.chunk_min = sp.chunk_min; p.chunk_max = sp.chunk_max; p.target_units = sp.target_units;
   // The skew is not applied to a fixed split, nor at head_dim 256: there the
   // even and odd XCDs stream at the same rate (16-bit KV: partial kernel
@@ -2468,13 +2497,13 @@ int fsk_paged_gather(const void* pool, int64_t stride_p, int64_t stride_h, int64
 #ifdef FSK_WAVE_STAMPS
 int fsk_debug_wave_stamps(uint64_t* out, int waves) {
   if (!out || waves < 0 || waves > kStampWaves) return fail(FSK_ERR_INVALID, "null pointer or waves out of range");
-  const hipError_t e = hipMemcpyFromSymbol(out, HIP_SYMBOL(g_wave_stamps), sizeof(uint64_t) * 8 * (size_t)waves);
+  const hipError_t e = hipMemcpyFromSymbol(out, HIP_SYMBOL(g_wave_stamps), sizeof(uint64_t) * kStampSlots * (size_t)waves);
   if (e != hipSuccess) return fail(FSK_ERR_HIP, std::string("hipMemcpyFromSymbol: ") + hipGetErrorString(e));
   return FSK_OK;
 }
 
 int fsk_debug_clear_wave_stamps(void) {
-  static const uint64_t zeros[kStampWaves * 8] = {0};
+  static const uint64_t zeros[kStampWaves * kStampSlots] = {0};
   const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_wave_stamps), zeros, sizeof(zeros));
   if (e != hipSuccess) return fail(FSK_ERR_HIP, std::string("hipMemcpyToSymbol: ") + hipGetErrorString(e));
   return FSK_OK;
@@ -2512,9 +2541,10 @@ int fsk_debug_split(int64_t total, int chunk_min, int chunk_max, int target_unit
   if (item_chunk && item_slot) {
     const int64_t W = (int64_t)sp.n * head_slots;
     if (W >= ((int64_t)1 << 31)) return fail(FSK_ERR_UNSUPPORTED, "too many work items");
+    const FastDiv nh = make_fastdiv((uint32_t)head_slots);
     for (int64_t w = 0; w < W; ++w) {
       int jc, hh;
-      item_of(sp, w, head_slots, jc, hh);
+      item_of(sp, (uint32_t)w, nh, jc, hh);
       item_chunk[w] = jc;
       item_slot[w] = hh;
     }

@@ -334,11 +334,12 @@ FSK_API int fsk_kernel_timing(double *partial_ms, double *total_ms, int64_t *cal
 
 /* Instrumented builds only (libfsk_decode_stamps.so, compiled with
  * -DFSK_WAVE_STAMPS; bench.py --wave-stamps): the partial kernel's per-wave
- * timeline of the last decode call.  out receives 8 uint64 per workgroup w <
- * waves: s_memrealtime (100 MHz) at the wave's start, plan done, first tile
+ * timeline of the last decode call.  out receives 16 uint64 per workgroup w
+ * < waves: s_memrealtime (100 MHz) at the wave's start, plan done, first tile
  * in registers, last epilogue issued and exit (0 where a stage did not
- * happen), the number of segments processed and the XCC id.  No reference
- * counterpart (measurement only). */
+ * happen), the number of segments processed, the XCC id, the HW_ID register,
+ * and (paged) the first item's page-window and Q loads issued and arrived;
+ * slots 10-15 are unused.  No reference counterpart (measurement only). */
 #ifdef FSK_WAVE_STAMPS
 FSK_API int fsk_debug_wave_stamps(uint64_t *out, int waves);
 FSK_API int fsk_debug_clear_wave_stamps(void);
