@@ -599,6 +599,23 @@ def test_batches_above_one_wave(layout):
     run_and_check(wl, chunk_tokens=64, what=f"{layout} B=150 chunk 64")
 
 
+@pytest.mark.parametrize("B", [63, 64, 65])
+@pytest.mark.parametrize("layout", ["varlen", "paged"])
+def test_batches_at_one_wave_with_empty_runs(layout, B):
+    """Batches around one wave (up to 64 sequences the work loop reads the
+    plan's tables from the lanes' registers, above from LDS), with runs of
+    empty sequences (repeated table entries) at the start, the middle and
+    the end, and short splits so that units start inside those runs."""
+    name = "C1" if layout == "varlen" else "C3"
+    lens = _lens(B, 300, 60 + B)
+    for i in (0, 1, 2, 30, 31, 32, 33, B - 2, B - 1):
+        lens[i] = 0
+    lens[B // 2] = 700
+    wl = W.make(name, overrides=dict(B=B, lens=("list", lens), sinks=True), seed=61)
+    run_and_check(wl, what=f"{layout} B={B}")
+    run_and_check(wl, chunk_tokens=32, what=f"{layout} B={B} chunk 32")
+
+
 @pytest.mark.parametrize("layout", ["varlen", "paged"])
 def test_maximum_batch(layout):
     """The largest batch the library takes (16384 sequences): the plan keeps
