@@ -329,8 +329,10 @@ __device__ __forceinline__ HalfTile half_tile(const Params& p, int b, int start,
 // u_max for chunk_max.  In LDS: flat[b] = stream offset of sequence b's
 // region (its first token sits seg_tokens later; flat[B] = stream length),
 // pre[b] = first partial of sequence b (pre[B] =
-// total).  Workgroup 0 publishes pre for the reduce kernel.  Every workgroup
-// computes the same plan from the same lengths.  Returns the chunk count.
+// total); lane b also returns its own entries flat[b] and pre[b] (the work
+// loop reads them from registers when B <= 64).  Workgroup 0 publishes pre
+// for the reduce kernel.  Every workgroup computes the same plan from the
+// same lengths.  Returns the chunk count.
 // Chunk geometry.  The stream is cut into pairs of a long chunk (c_e tokens)
 // and a short one (c_o); c_e == c_o without an XCD skew.  Chunk j starts at
 // (j / 2) * (c_e + c_o) + (j odd ? c_e : 0).
