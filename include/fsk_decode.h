@@ -298,7 +298,8 @@ FSK_API int fsk_debug_split(int64_t total, int chunk_min, int chunk_max,
  *   "waves_per_cu"        persistent grid size, workgroups per CU (default 8)
  *   "target_waves_per_cu" automatic split: units of work per CU (default 4)
  *   "xcd_skew"            automatic split: extra share of the even XCDs, in %
- *                         (0..50, default 3; 0 = equal chunks)
+ *                         (0..50, default 3; 0 = equal chunks; not applied at
+ *                         head_dim 256, nor to a fixed chunk_tokens split)
  *   "seg_tokens"          work-stream positions laid before each sequence when
  *                         non-empty lengths differ and there are at most 8
  *                         chunks per sequence, so that items holding a
