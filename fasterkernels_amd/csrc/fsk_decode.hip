@@ -374,6 +374,7 @@ __host__ __device__ __forceinline__ void item_of(const Split& sp, uint32_t w, Fa
 }
 
 constexpr int kSkewMinChunk = 512;  // smallest split that gets the XCD skew (tokens)
+constexpr int kShortChunk = 64;     // smallest automatic split of a short stream (tokens)
 
 // The scalar part of the plan: the chunk geometry of a stream of `total`
 // padded tokens (align = the padding, 32 or 128).  Compiled for the host too,
@@ -400,11 +401,28 @@ __host__ __device__ __forceinline__ Split split_geometry(uint32_t total, const S
   const uint32_t t_need = cdiv(total, chunk_max);
   uint32_t target = (uint32_t)a.target_units;
   while (target < t_need && target < (1u << 24)) target *= 2;
+  auto up = [&](uint32_t x) { return (x + align - 1) / align * align; };
   uint32_t want = cdiv(total, target);
-  const uint32_t cap = a.u_max > a.B + 1 ? (uint32_t)(a.u_max - a.B - 1) : 0;  // chunks the workspace holds
-  want = cap > 0 ? umax(want, cdiv(total, cap)) : chunk_max;
-  want = (want + align - 1) / align * align;
-  const uint32_t chunk = umin(umax(want, (uint32_t)a.chunk_min), chunk_max);
+  uint32_t lo = (uint32_t)a.chunk_min, hi = chunk_max;
+  if (want < lo && a.chunk_min < a.chunk_max) {
+    // A short stream (target chunks would be below chunk_min): half as many
+    // chunks, of kShortChunk to chunk_min tokens.  Items of 2-3 tiles
+    // finished sooner than both 4-tile items (fewer waves, twice the round
+    // trips each) and 1-tile items (per-item costs).  Only while that keeps
+    // to 32 chunks per sequence on average: the reduce merges 32 partials of
+    // a sequence per memory round trip (head_dim 128).
+    const uint32_t w2 = cdiv(total, umax(target / 2, 1u));
+    const uint32_t lo2 = up((uint32_t)kShortChunk), hi2 = umax((uint32_t)a.chunk_min, lo2);
+    if (cdiv(total, umin(umax(up(w2), lo2), hi2)) <= 32u * (uint32_t)a.B) {
+      want = w2;
+      lo = lo2;
+      hi = hi2;
+    }
+  }
+  uint32_t chunk = umin(umax(up(want), lo), hi);
+  // at most `cap` chunks: every partial must fit the workspace
+  const uint32_t cap = a.u_max > a.B + 1 ? (uint32_t)(a.u_max - a.B - 1) : 0;
+  chunk = cap > 0 ? umin(umax(chunk, up(cdiv(total, cap))), chunk_max) : chunk_max;
   Split sp;
   sp.c_e = sp.c_o = (int)chunk;
   sp.n = (int)cdiv(total, chunk);
@@ -1759,8 +1777,14 @@ SplitPlan plan_split(int layout, int B, int64_t nh, int64_t kv_extent, int page_
   const int64_t target = std::max<int64_t>(1, (int64_t)cus * g_opt.target_waves_per_cu / nh);
   sp.target_units = (int)std::min<int64_t>(target, 1 << 20);
   const int64_t cap = std::max<int64_t>(4 * target, 256);
-  sp.u_max = std::max(unit_bound(layout, B, kv_extent, page_size, kChunkMax),
-                      std::min(unit_bound(layout, B, kv_extent, page_size, kChunkMin), cap));
+  // Room for short-stream splits (chunks down to kShortChunk, at most 32 per
+  // sequence on average) only where the device can choose them: the
+  // workspace bound also sizes the persistent grid.
+  int64_t u_plan = unit_bound(layout, B, kv_extent, page_size, kChunkMin);
+  if (stream_bound(layout, B, kv_extent, page_size) < target * kChunkMin)
+    u_plan = std::max(u_plan, std::min(unit_bound(layout, B, kv_extent, page_size, kShortChunk),
+                                       33 * (int64_t)B + 1));
+  sp.u_max = std::max(unit_bound(layout, B, kv_extent, page_size, kChunkMax), std::min(u_plan, cap));
   return sp;
 }
 

@@ -3,8 +3,9 @@
 fsk_debug_split runs the same split_geometry / chunk_lo / chunk_of / item_of
 code that every workgroup of the partial kernel runs, compiled for the host.
 The split policy arguments are the ones a decode call passes (automatic
-splits: chunk bounds 128..4096 tokens, 4 items per CU, the workspace capacity
-the host sizes; fixed splits: one chunk size, no XCD skew).  Checked: chunk
+splits: chunk bounds 128..4096 tokens, down to 64 for short streams, 4 items
+per CU, the workspace capacity the host sizes; fixed splits: one chunk size,
+no XCD skew).  Checked: chunk
 sizes and alignment, contiguous coverage of the token stream, the token ->
 chunk map, room for every partial in the workspace, and that work items map
 one-to-one onto (chunk, head slot) pairs with the long chunks on even XCDs.
@@ -17,7 +18,7 @@ import pytest
 
 from fasterkernels_amd import native as nat
 
-CHUNK_MIN, CHUNK_MAX, SKEW_MIN = 128, 4096, 512
+CHUNK_MIN, CHUNK_MAX, SKEW_MIN, SHORT_CHUNK = 128, 4096, 512, 64
 
 
 def cdiv(a, b):
@@ -36,7 +37,10 @@ def host_policy(total, B, NH, cus, fixed=0, skew=3):
         return fixed, fixed, 1, unit_bound(fixed), 0
     target = max(1, cus * 4 // NH)
     cap = max(4 * target, 256)
-    return CHUNK_MIN, CHUNK_MAX, target, max(unit_bound(CHUNK_MAX), min(unit_bound(CHUNK_MIN), cap)), skew
+    u_plan = unit_bound(CHUNK_MIN)
+    if bound < target * CHUNK_MIN:
+        u_plan = max(u_plan, min(unit_bound(SHORT_CHUNK), 33 * B + 1))
+    return CHUNK_MIN, CHUNK_MAX, target, max(unit_bound(CHUNK_MAX), min(u_plan, cap)), skew
 
 
 def split(total, cmin, cmax, target, u_max, B, skew, NH, align):
@@ -63,7 +67,9 @@ def check_case(total, B, NH, cus, fixed, skew, align):
         assert skew > 0 and co < ce and (ce + co) % 2 == 0 and (ce + co) // 2 >= SKEW_MIN, what
         assert n % 2 == 0 and (n * NH) % 8 == 0, what
     else:
-        assert ce == co and cmin <= ce <= cmax, what
+        # automatic splits of short streams go down to SHORT_CHUNK (rounded to align)
+        lo = cmin if cmin == cmax else min(cmin, cdiv(SHORT_CHUNK, align) * align)
+        assert ce == co and lo <= ce <= cmax, what
     # contiguous coverage of [0, total): chunk j starts where chunk j-1 ends
     lens = np.where(np.arange(n) % 2 == 0, ce, co)
     assert n == len(starts)
@@ -119,6 +125,19 @@ def test_split_m0_geometry():
     128 chunks, the long ones on the even XCDs."""
     ce, co, n, paired, *_ = split(131072, *host_policy(131072, 4, 8, 256)[:4], 4, 3, 8, 32)
     assert (ce, co, n, paired) == (1056, 992, 128, True)
+
+
+@pytest.mark.parametrize("total,B,want", [(5120, 4, 96), (4096, 4, 64), (2048, 4, 64), (8192, 4, 128),
+                                          (16384, 4, 128), (4096, 1, 128), (2048, 1, 64), (4096, 2, 64)])
+def test_split_short_streams(total, B, want):
+    """Streams too short for 128 chunks of 128 tokens (8 KV heads, 256 CUs)
+    take half as many chunks, of 64 to 128 tokens, while that averages at
+    most 32 chunks per sequence; from 8192 tokens up the split is the plain
+    128-token one.  Block scores (align 128) keep 128."""
+    ce, co, n, paired, *_ = split(total, *host_policy(total, B, 8, 256)[:4], B, 3, 8, 32)
+    assert (ce, co, paired) == (want, want, False) and n == cdiv(total, want)
+    ce, *_ = split(total, *host_policy(total, B, 8, 256)[:4], B, 3, 8, 128)
+    assert ce == 128
 
 
 def test_split_random_policies():
