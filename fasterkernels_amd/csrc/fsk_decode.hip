@@ -1737,7 +1737,7 @@ int device_cus() {
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
-constexpr int kChunkMin = 128;   // smallest automatic split (tokens)
+constexpr int kChunkMin = 128;   // floor of an automatic split (tokens; short streams go down to kShortChunk)
 constexpr int kSegTokensMax = 256;  // largest lead-in per sequence (tokens)
 constexpr int kChunkMax = 4096;  // largest split: 256 pages of 16 tokens per paged unit (the page window)
 
