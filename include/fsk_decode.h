@@ -295,7 +295,9 @@ FSK_API int fsk_debug_split(int64_t total, int chunk_min, int chunk_max,
 
 /* Tuning knobs for benchmarking sweeps:
  *   "chunk_tokens"        fixed split size in tokens (0: chosen on the device)
- *   "waves_per_cu"        persistent grid size, workgroups per CU (default 8)
+ *   "waves_per_cu"        largest persistent grid, workgroups per CU (default
+ *                         8; the grid also stops at the work items the split
+ *                         can plan)
  *   "target_waves_per_cu" automatic split: units of work per CU (default 4)
  *   "xcd_skew"            automatic split: extra share of the even XCDs, in %
  *                         (0..50, default 3; 0 = equal chunks; not applied at

@@ -87,6 +87,12 @@ def check_case(total, B, NH, cus, fixed, skew, align):
     assert np.array_equal(tok, np.searchsorted(starts, x, side="right") - 1), what
     # every partial fits: at most n + B of them, and the workspace holds u_max
     assert n + B + 1 <= u_max, what
+    # at most the target count of chunks (doubled while chunks would exceed
+    # chunk_max) plus one: the host sizes the persistent grid on this bound
+    t = target
+    while t < cdiv(total, cmax) and t < (1 << 24):
+        t *= 2
+    assert n <= t + 1, what
     # work items: a bijection onto (chunk, head slot), long chunks on even XCDs
     assert ((ic >= 0) & (ic < n) & (isl >= 0) & (isl < NH)).all(), what
     assert len(np.unique(ic.astype(np.int64) * NH + isl)) == n * NH, what
