@@ -500,6 +500,14 @@ def test_c4_full_size():
     run_and_check(wl, what="C4")
 
 
+@pytest.mark.parametrize("name", ["M0b", "G1", "G2"])
+def test_other_bench_workloads_full_size(name):
+    """The bench's other decode workloads at their bench sizes: M0 in bf16
+    (Q, KV and output), varlen at head_dim 64 with sinks (KV head pairs, 4 x
+    65536 tokens) and paged at head_dim 256 (4 x 16384 tokens)."""
+    run_and_check(W.make(name), what=name)
+
+
 @pytest.fixture(scope="module")
 def c5_full():
     return W.make("C5")
