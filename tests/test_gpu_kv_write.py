@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 import torch
 
+from fasterkernels_amd import workloads as W
 from fskernels.hip import paged_kv_write
 from fskernels.paged_attn import PagedKVCache, paged_flash_decode
 from fskernels.hip import decode as dec
@@ -458,3 +459,24 @@ def test_rejected_append_leaves_cache_unchanged_and_host_rows_are_copied():
     assert torch.equal(cache.block_table, bt)
     assert torch.equal(cache.block_table, twin.block_table) and cache._seq_lens == twin._seq_lens
     assert torch.equal(cache.k_pool.cpu(), twin.k_pool.cpu()) and torch.equal(cache.v_pool.cpu(), twin.v_pool.cpu())
+
+
+@pytest.mark.parametrize("name", ["W0", "W1", "W2"])
+def test_bench_write_workloads(name):
+    """The bench's KV-write workloads at their bench sizes, bit-exact against
+    the oracle: W0 the whole M0 cache (131072 tokens) f16 -> f16, W1 the same
+    rows bf16 -> e4m3 with scales, W2 one decode-step append for 64
+    sequences (rows into partly filled pages of a zeroed pool)."""
+    wl = W.make_write(name, device=DEV)
+    cfg = W.WRITE_CONFIGS[name]
+    W.run_write(wl)
+    torch.cuda.synchronize()
+    slots = wl.slots.cpu().numpy()
+    for x, got, sc, kv in ((wl.k, wl.k_pool, wl.k_scale, "K"), (wl.v, wl.v_pool, wl.v_scale, "V")):
+        if cfg["pool"] == "e4m3":
+            o = np.zeros(tuple(got.shape), np.uint8)
+            O.paged_write(o, slots, x.float().cpu().numpy(), "e4m3", None if sc is None else np.float32(sc.item()))
+        else:
+            o = np.zeros(tuple(got.shape), np.float16)
+            O.paged_store_rows(o.view(np.uint16), slots, x.view(torch.int16).cpu().numpy().view(np.uint16))
+        compare(got, o, cfg["pool"], cfg["src"], f"{kv} {name}")
