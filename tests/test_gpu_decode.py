@@ -508,6 +508,33 @@ def test_other_bench_workloads_full_size(name):
     run_and_check(W.make(name), what=name)
 
 
+@pytest.mark.parametrize("name", ["C3", "C5"])
+def test_full_size_constant_values(name):
+    """A size-independent property at the bench sizes, checked without the
+    oracle: when every V row of a KV head holds the same vector c, each query
+    head's output is c whatever its scores and however the batch is split
+    (without sinks the weights sum to 1).  C3: 32 ragged sequences on
+    shuffled pages; C5: 64 lognormal sequences with e4m3 KV (c = a random
+    code per dim times the V scale)."""
+    wl = W.make(name)
+    wl.s_aux = None
+    g = torch.Generator().manual_seed(5)
+    Hkv, D = wl.Hkv, wl.D
+    if wl.v.dtype == torch.float8_e4m3fn:
+        codes = (torch.randint(0, 0x7F, (Hkv, D), generator=g) |
+                 (torch.randint(0, 2, (Hkv, D), generator=g) << 7)).to(torch.uint8)
+        c = O.e4m3_decode(codes.numpy()).astype(np.float64) * float(wl.v_scale)
+        wl.v.view(torch.uint8)[:] = codes[None, :, None, :]
+    else:
+        cv = torch.randn(Hkv, D, generator=g).to(wl.v.dtype)
+        c = f64(cv)
+        wl.v[:] = cv[None, :, None, :]
+    ref = np.repeat(c, wl.Hq // Hkv, axis=0)[None].repeat(wl.B, axis=0)
+    out = W.run(wl.to(DEV))
+    torch.cuda.synchronize()
+    assert_close(out, ref, 2e-3, 2e-3, f"{name} with constant V rows")
+
+
 @pytest.fixture(scope="module")
 def c5_full():
     return W.make("C5")
