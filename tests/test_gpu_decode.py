@@ -755,6 +755,37 @@ def test_randomized_configurations(seed):
     run_and_check(wl, chunk_tokens=chunk, what=f"seed {seed}: {name} {ov} chunk={chunk}")
 
 
+def _random_large_case(seed):
+    """A random large batch: 9-300 sequences (5 % empty, 10 % of 1-16
+    tokens, the rest lognormal up to 32768), at most ~600K tokens per call."""
+    r = np.random.default_rng(seed)
+    layout = ["M0", "C1"][r.integers(2)]
+    kv = ["f16", "bf16", "e4m3"][r.integers(3)]
+    q = "bf16" if kv == "bf16" else ["f16", "bf16"][r.integers(2)] if kv == "e4m3" else "f16"
+    Hkv, G, D = int(r.choice([1, 2, 8])), int(r.choice([1, 4, 8])), int(r.choice([64, 128, 256]))
+    B = int(r.integers(9, 301))
+    mean = max(1, int(min(600_000, 3e8 / (Hkv * D * G))) // B)
+    lens = []
+    for _ in range(B):
+        u = r.random()
+        lens.append(0 if u < 0.05 else int(r.integers(1, 17)) if u < 0.15
+                    else int(min(32768, r.lognormal(np.log(mean), 1.0))))
+    if sum(lens) == 0:
+        lens[0] = 7
+    chunk = int(r.choice([0, 0, 0, 64, 512, 4096]))
+    return layout, dict(B=B, Hq=G * Hkv, Hkv=Hkv, D=D, q=q, kv=kv, out=q, sinks=bool(r.integers(2)),
+                        lens=("list", lens)), chunk
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_randomized_large_batches(seed):
+    """Batches past one wave of sequences (plan tables in LDS), with lead-ins
+    and several items per wave where the split gives them."""
+    name, ov, chunk = _random_large_case(20000 + seed)
+    wl = W.make(name, overrides=ov, seed=seed)
+    run_and_check(wl, chunk_tokens=chunk, what=f"seed {seed}: {name} B={ov['B']} chunk={chunk}")
+
+
 @pytest.mark.parametrize("seed", range(20))
 def test_randomized_dense_configurations(seed):
     """Dense HF-cache layout: random batch, cache size, lengths, start offsets,
