@@ -43,6 +43,9 @@ def compile_flags() -> list[str]:
         "-shared",
         # Packed-FP32 VALU ops are kept out of the generated code on purpose.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # The leading scalar/pointer kernel arguments (the partial kernel's
+        # lengths pointers and batch) arrive in SGPRs at dispatch.
+        "-mllvm", "-amdgpu-kernarg-preload-count=3",
         "-fvisibility=hidden",
         f"-Wl,-soname,{LIB_NAME}",
         f"-I{INCLUDE}",

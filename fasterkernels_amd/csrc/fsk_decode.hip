@@ -447,6 +447,29 @@ __host__ __device__ __forceinline__ Split split_geometry(uint32_t total, const S
   return sp;
 }
 
+// seq_range of sequence `lane` (0 for lanes at or past B) with its loads
+// issued unconditionally (index clamped to B - 1; B >= 1), so that they go
+// out before the kernel arguments they are clamped with have arrived.
+template <int kLayout>
+__device__ __forceinline__ void seq_range_first(const Params& p, int lane, int& start, int& len) {
+  const int b = min(lane, p.B - 1);
+  const int l0 = p.lens[b];
+  const int l1 = kLayout == kVarlen ? p.lens[b + 1] : 0;
+  const int s0 = (kLayout == kDense && p.starts) ? p.starts[b] : 0;
+  if constexpr (kLayout == kVarlen) {
+    start = clampi(l0, 0, p.kv_extent);
+    len = clampi(l1, start, p.kv_extent) - start;
+  } else if constexpr (kLayout == kPaged) {
+    start = 0;
+    len = clampi(l0, 0, p.max_blocks * p.page_size);
+  } else {
+    const int e = clampi(l0, 0, p.kv_extent);
+    start = p.starts ? clampi(s0, 0, e) : 0;
+    len = e - start;
+  }
+  if (lane >= p.B) start = len = 0;
+}
+
 template <int kLayout, bool kScores>
 __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32_t* flat, int& start0_out,
                                             int& len0_out, int& seg_out, int& flat0_out, int& pre0_out) {
@@ -456,7 +479,7 @@ __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32
   // register so that the common case (B <= 64) reads them once (and the
   // work loop reads them from these registers, not from memory).
   int len0 = 0, start0 = 0;
-  if (lane < p.B) seq_range<kLayout>(p, lane, start0, len0);
+  seq_range_first<kLayout>(p, lane, start0, len0);
   start0_out = start0;
   len0_out = len0;
   auto length = [&](int b0, int b) {
@@ -994,7 +1017,16 @@ __device__ __forceinline__ void compute_tile_valu(const TileRegs<D, kF16>& T, ui
 constexpr int kWavesPerEu = FSK_PIPE_DEPTH > 2 ? 1 : 2;
 
 template <int D, int kQ, int kKV, int kLayout, bool kScores, bool kValu = false>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu))) void partial_kernel(Params p) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu))) void partial_kernel(
+    const int32_t* lens_arg, const int32_t* starts_arg, int B_arg, Params pk) {
+  // The plan's first loads (the lengths) need only these three, which lead
+  // the argument list so that the dispatch preloads them into SGPRs
+  // (-amdgpu-kernarg-preload-count): the length loads issue without waiting
+  // for a kernel-argument load.
+  Params p = pk;
+  p.lens = lens_arg;
+  p.starts = starts_arg;
+  p.B = B_arg;
   using TR = TileRegs<D, kKV>;
   using SM = Softmax<D, kQ, kKV>;
   constexpr bool kKvFp8 = TR::kFp8;
@@ -1932,7 +1964,7 @@ void launch(K kernel, dim3 grid, dim3 block, uint32_t lds, const Launch& L, Args
 
 template <int D, int kQ, int kKV, int kLayout, bool kScores>
 void launch_partial(const Params& p, int grid, const Launch& s) {
-  launch(partial_kernel<D, kQ, kKV, kLayout, kScores>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p);
+  launch(partial_kernel<D, kQ, kKV, kLayout, kScores>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p.lens, p.starts, p.B, p);
 }
 
 template <int D, int kLayout, bool kScores>
@@ -1949,9 +1981,9 @@ int dispatch_qkv(const Params& p, int grid, int q_dt, int kv_dt, const Launch& s
 // The VALU-tile kernels (option qk_engine = 1; f16, D = 128, paged or varlen).
 int launch_valu(int layout, const Params& p, int grid, const Launch& s) {
   if (layout == FSK_LAYOUT_PAGED)
-    launch(partial_kernel<128, kF16, kF16, kPaged, false, true>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p);
+    launch(partial_kernel<128, kF16, kF16, kPaged, false, true>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p.lens, p.starts, p.B, p);
   else
-    launch(partial_kernel<128, kF16, kF16, kVarlen, false, true>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p);
+    launch(partial_kernel<128, kF16, kF16, kVarlen, false, true>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p.lens, p.starts, p.B, p);
   return FSK_OK;
 }
 
