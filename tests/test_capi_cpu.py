@@ -318,7 +318,10 @@ def test_partial_kernels_keep_uniform_state_in_scalars():
     (scratch) memory and no readfirstlane loop around a buffer load, which
     this compiler emits when a buffer resource is built from a value it
     cannot prove uniform (a select lowered to a table in scratch, a value
-    leaving a loop whose bound came out of a wave shuffle)."""
+    leaving a loop whose bound came out of a wave shuffle).  And each takes
+    its lengths pointers and batch size preloaded in SGPRs (5 dwords), its
+    first memory instruction past the preload prologue being a length load,
+    not a kernel-argument load."""
     from fasterkernels_amd import build
     res = subprocess.run([build.hipcc(), *[f for f in build.compile_flags() if f not in ("-shared", "-fPIC")],
                           "--cuda-device-only", "-S", build.SRC, "-o", "-"],
@@ -334,6 +337,10 @@ def test_partial_kernels_keep_uniform_state_in_scalars():
         scratch = int(re.search(r"amdhsa_private_segment_fixed_size (\d+)", meta).group(1))
         waterfalls = len(re.findall(r"v_cmp_eq_u64_e32 vcc, s\[\d+:\d+\], v\[", body))
         assert scratch == 0 and waterfalls == 0, (name, scratch, waterfalls)
+        preload = int(re.search(r"amdhsa_user_sgpr_kernarg_preload_length (\d+)", meta).group(1))
+        entry = body.split("s_branch", 1)[1]
+        first = re.search(r"^\s+((?:global|buffer|flat|s)_load\w*)", entry, re.M).group(1)
+        assert preload == 5 and first.startswith("global_load"), (name, preload, first)
 
 
 def test_xcd_skew_option(lib):
