@@ -1964,7 +1964,8 @@ void launch(K kernel, dim3 grid, dim3 block, uint32_t lds, const Launch& L, Args
 
 template <int D, int kQ, int kKV, int kLayout, bool kScores>
 void launch_partial(const Params& p, int grid, const Launch& s) {
-  launch(partial_kernel<D, kQ, kKV, kLayout, kScores>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p.lens, p.starts, p.B, p);
+  launch(partial_kernel<D, kQ, kKV, kLayout, kScores>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p.lens, p.starts,
+         p.B, p);
 }
 
 template <int D, int kLayout, bool kScores>
@@ -1981,9 +1982,11 @@ int dispatch_qkv(const Params& p, int grid, int q_dt, int kv_dt, const Launch& s
 // The VALU-tile kernels (option qk_engine = 1; f16, D = 128, paged or varlen).
 int launch_valu(int layout, const Params& p, int grid, const Launch& s) {
   if (layout == FSK_LAYOUT_PAGED)
-    launch(partial_kernel<128, kF16, kF16, kPaged, false, true>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p.lens, p.starts, p.B, p);
+    launch(partial_kernel<128, kF16, kF16, kPaged, false, true>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p.lens,
+           p.starts, p.B, p);
   else
-    launch(partial_kernel<128, kF16, kF16, kVarlen, false, true>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p.lens, p.starts, p.B, p);
+    launch(partial_kernel<128, kF16, kF16, kVarlen, false, true>, dim3(grid), dim3(64), 8 * (p.B + 1), s, p.lens,
+           p.starts, p.B, p);
   return FSK_OK;
 }
 
