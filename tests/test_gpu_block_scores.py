@@ -121,3 +121,30 @@ def test_binding_rejects_bad_score_tensors():
     out = ext.varlen(q, k, v, cu, None, None, None, -1, 0, None, 0, good, stream)
     torch.cuda.synchronize()
     assert out.shape == (2, 32, 128) and torch.isfinite(good.float()).all()
+
+
+@pytest.mark.parametrize("name", ["M0", "C2"])
+def test_block_scores_bench_sizes(name):
+    """The `--block-scores` bench workloads at their sizes: M0 (paged, 4 x
+    32768 tokens: 128-token-rounded chunk pairs of the XCD skew) and C2
+    (varlen with exp sinks), scores and output against the oracle."""
+    wl = W.make(name)
+    d = wl.to(DEV)
+    if wl.layout == "paged":
+        out, S = paged_flash_decode(d.q, d.k, d.v, d.block_table, d.seq_lens, 16, s_aux=d.s_aux,
+                                    return_block_scores=True)
+        want = O.block_scores_paged(wl.q.double().numpy(), wl.k.numpy(), wl.block_table.numpy(), wl.lens,
+                                    None if wl.s_aux is None else wl.s_aux.double().numpy(), "exp",
+                                    n_blocks=S.shape[2])
+        ref = O.decode_paged(wl.q.double().numpy(), wl.k.numpy(), wl.v.numpy(), wl.block_table.numpy(), wl.lens,
+                             None if wl.s_aux is None else wl.s_aux.double().numpy())
+    else:
+        out, S = flash_decode_gqa_varlen(d.q, d.k, d.v, d.cu_seqlens, d.s_aux, return_block_scores=True)
+        want = O.block_scores_varlen(wl.q.double().numpy(), wl.k.numpy(), wl.cu_seqlens.numpy(),
+                                     wl.s_aux.double().numpy(), "exp", n_blocks=S.shape[2])
+        ref = O.decode_varlen(wl.q.double().numpy(), wl.k.double().numpy(), wl.v.double().numpy(),
+                              wl.cu_seqlens.numpy(), wl.s_aux.double().numpy())
+    torch.cuda.synchronize()
+    close(S, want, f"{name} block scores")
+    o = out.double().cpu().numpy()
+    assert (np.abs(o - ref) <= 2e-3 + 2e-3 * np.abs(ref) + np.abs(ref) * 2.0 ** -11).all(), f"{name} output"
