@@ -1351,6 +1351,19 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) 
   const int n = p.plan[b + 1] - u0;
   const int64_t base = ((int64_t)u0 * p.Hkv + kvh) * p.G + hg;  // partial index of unit u0
   const int64_t ustride = (int64_t)p.Hkv * p.G;                 // between consecutive units
+  // Block scores: every thread loads up to kScorePre of this row's block
+  // maxima now, in the same round trip as the partials, and stores their
+  // scores once the denominator is known.
+  constexpr int kScorePre = 4;
+  float bmax[kScorePre];
+  if (p.scores) {
+    const float* src = p.blk_max + ((int64_t)b * p.Hq + h) * p.nblk;
+#pragma unroll
+    for (int i = 0; i < kScorePre; ++i) {
+      const int j = tid + i * kReduceThreads;
+      bmax[i] = j < p.nblk ? src[j] : -INFINITY;
+    }
+  }
 
   float m_t = -INFINITY, l_t = 0.f;
   f32x4 a_t = {0.f, 0.f, 0.f, 0.f};
@@ -1394,15 +1407,13 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) 
   s_acc[grp][d4] = a_t * f;
   if (d4 == 0) s_l[grp] = l_t * f;
   __syncthreads();
-  if (grp != 0) return;
-  f32x4 num = s_acc[0][d4];
+  // The denominator (every thread when block scores need it), then the
+  // numerator (group 0, which stores the output row).
+  if (grp != 0 && !p.scores) return;
   float den = s_l[0];
 #pragma unroll
-  for (int q = 1; q < kGroups; ++q) {
-    num += s_acc[q][d4];
-    den += s_l[q];
-  }
-
+  for (int q = 1; q < kGroups; ++q) den += s_l[q];
+  float fs = 1.f;     // scale of the numerator for an exp sink
   float ref = M_use;  // reference point of den
   if (p.s_aux) {
     if (p.sink_mode == FSK_SINK_EXP) {
@@ -1411,9 +1422,8 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) 
       const float Mn = fmaxf(M, z2);
       const float Mn_use = (Mn == -INFINITY) ? 0.f : Mn;
       // An empty sequence (M = -inf, num = den = 0) keeps a zero numerator.
-      const float fs = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - Mn_use);
+      fs = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - Mn_use);
       den = den * fs + __builtin_amdgcn_exp2f(z2 - Mn_use);
-      num *= fs;
       ref = Mn_use;
     } else {
       den += z;  // linear fold relative to the running max (flash_decode_cuda.cu:151-153)
@@ -1425,13 +1435,24 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) 
     const float inv = 1.f / den;
     const float* src = p.blk_max + ((int64_t)b * p.Hq + h) * p.nblk;
     uint8_t* dst = p.scores + ((int64_t)b * p.Hq + h) * p.nblk * (kOut == kF32 ? 4 : 2);
-    for (int j = d4; j < p.nblk; j += kD4) {
-      const float sc = j < nvalid ? __builtin_amdgcn_exp2f(src[j] - ref) * inv : 0.f;
+    auto put = [&](int j, float mx) {
+      const float sc = j < nvalid ? __builtin_amdgcn_exp2f(mx - ref) * inv : 0.f;
       if constexpr (kOut == kF32) ((float*)dst)[j] = sc;
       else if constexpr (kOut == kF16) ((f16*)dst)[j] = (f16)sc;
       else ((bf16*)dst)[j] = (bf16)sc;
+    };
+#pragma unroll
+    for (int i = 0; i < kScorePre; ++i) {
+      const int j = tid + i * kReduceThreads;
+      if (j < p.nblk) put(j, bmax[i]);
     }
+    for (int j = tid + kScorePre * kReduceThreads; j < p.nblk; j += kReduceThreads) put(j, src[j]);
   }
+  if (grp != 0) return;
+  f32x4 num = s_acc[0][d4];
+#pragma unroll
+  for (int q = 1; q < kGroups; ++q) num += s_acc[q][d4];
+  if (p.s_aux && p.sink_mode == FSK_SINK_EXP) num *= fs;
 
   uint8_t* o = p.out + (int64_t)b * p.o_sb + (int64_t)h * p.o_sh;
   const f32x4 val = num / den;
