@@ -1830,26 +1830,30 @@ struct SplitPlan {
 };
 SplitPlan plan_split(int layout, int B, int64_t nh, int64_t kv_extent, int page_size, int chunk_tokens, int cus) {
   SplitPlan sp;
-  const int fixed = chunk_tokens > 0 ? chunk_tokens : g_opt.chunk_tokens;
+  const int fixed = chunk_tokens > 0 ? chunk_tokens : chunk_tokens == 0 ? g_opt.chunk_tokens : 0;
   if (fixed > 0) {
     sp.chunk_min = sp.chunk_max = fixed;
     sp.target_units = 1;
     sp.u_max = unit_bound(layout, B, kv_extent, page_size, fixed);
     return sp;
   }
-  sp.chunk_min = kChunkMin;
-  sp.chunk_max = kChunkMax;
+  // chunk_tokens < 0: an automatic split of chunks of at most -chunk_tokens
+  // tokens (the dense entry points' split-count hint)
+  // (below 128 tokens the floor is the short-stream one, so that a cap never
+  // makes a split coarser than the uncapped choice)
+  sp.chunk_max = chunk_tokens < 0 && chunk_tokens > -kChunkMax ? -chunk_tokens : kChunkMax;
+  sp.chunk_min = sp.chunk_max >= kChunkMin ? kChunkMin : std::min(kShortChunk, sp.chunk_max);
   const int64_t target = std::max<int64_t>(1, (int64_t)cus * g_opt.target_waves_per_cu / nh);
   sp.target_units = (int)std::min<int64_t>(target, 1 << 20);
   const int64_t cap = std::max<int64_t>(4 * target, 256);
   // Room for short-stream splits (chunks down to kShortChunk, at most 32 per
   // sequence on average) only where the device can choose them: the
   // workspace bound also sizes the persistent grid.
-  int64_t u_plan = unit_bound(layout, B, kv_extent, page_size, kChunkMin);
+  int64_t u_plan = unit_bound(layout, B, kv_extent, page_size, sp.chunk_min);
   if (stream_bound(layout, B, kv_extent, page_size) < target * kChunkMin)
     u_plan = std::max(u_plan, std::min(unit_bound(layout, B, kv_extent, page_size, kShortChunk),
                                        33 * (int64_t)B + 1));
-  sp.u_max = std::max(unit_bound(layout, B, kv_extent, page_size, kChunkMax), std::min(u_plan, cap));
+  sp.u_max = std::max(unit_bound(layout, B, kv_extent, page_size, sp.chunk_max), std::min(u_plan, cap));
   return sp;
 }
 
@@ -1965,7 +1969,7 @@ int validate(const Common& c) {
     if (c.layout == FSK_LAYOUT_DENSE) return fail(FSK_ERR_UNSUPPORTED, "block scores on the varlen and paged layouts only");
     if (c.nblk <= 0 || c.nblk > (1 << 24)) return fail(FSK_ERR_INVALID, "score_blocks must be in [1, 2^24]");
     if (!aligned(c.scores, elem_bytes(c.o_dt))) return fail(FSK_ERR_INVALID, "scores must be aligned to the output dtype");
-    if (c.chunk % 128) return fail(FSK_ERR_INVALID, "with block scores chunk_tokens must be 0 or a multiple of 128");
+    if (c.chunk % 128) return fail(FSK_ERR_INVALID, "with block scores chunk_tokens must be a multiple of 128");
   }
   return FSK_OK;
 }
@@ -2045,7 +2049,7 @@ int run_decode(const Common& c) {
   const int G = c.Hq / c.Hkv;
   const int n_hb = (G + 15) / 16;
   const int cus = device_cus();
-  if (c.chunk < 0 || c.chunk % 32 != 0) return fail(FSK_ERR_INVALID, "chunk_tokens must be 0 or a positive multiple of 32");
+  if (c.chunk % 32 != 0) return fail(FSK_ERR_INVALID, "chunk_tokens must be a multiple of 32");
   const SplitPlan sp = plan_split(c.layout, c.B, plan_heads(c.layout, c.D, c.Hkv, G), c.kv_extent, c.page_size,
                                   c.chunk, cus);
   const bool pair =
@@ -2338,7 +2342,7 @@ int64_t fsk_workspace_bytes(int layout, int batch, int num_q_heads, int num_kv_h
   if (batch > kMaxBatch) return fail(FSK_ERR_UNSUPPORTED, "batch above 16384");
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return fail(FSK_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256");
   if (layout == FSK_LAYOUT_PAGED && (page_size <= 0 || page_size % 16)) return fail(FSK_ERR_UNSUPPORTED, "page_size must be a positive multiple of 16");
-  if (chunk_tokens < 0 || chunk_tokens % 32) return fail(FSK_ERR_INVALID, "chunk_tokens: 0 or a multiple of 32");
+  if (chunk_tokens % 32) return fail(FSK_ERR_INVALID, "chunk_tokens: a multiple of 32");
   const int G = num_q_heads / num_kv_heads;
   const int B = batch > 0 ? batch : 1;
   const SplitPlan sp = plan_split(layout, B, plan_heads(layout, head_dim, num_kv_heads, G), kv_extent, page_size,

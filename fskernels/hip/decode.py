@@ -29,9 +29,10 @@ def set_num_splits(n: int) -> None:
     """Split-count hint for flash_decode_gqa_hf_dense_optimized.
 
     The HIP kernels always split the KV sequence across the GPU with a device
-    work list; a value above 1 caps the number of splits per sequence (the
-    split size becomes ceil(S_max / n) rounded up to 32 tokens), 1 leaves the
-    split size to the library.  Mirrors fskernels/triton/triton_gqa_decode_hf.py:12-14.
+    work list; a value n above 1 makes every full-length sequence split into
+    at least n parts (chunks of at most ceil(S_max / n) tokens, rounded up to
+    32), finer where the GPU needs more work items; 1 leaves the split to the
+    library.  Mirrors fskernels/triton/triton_gqa_decode_hf.py:12-14.
     """
     global _DECODE_NUM_SPLITS
     _DECODE_NUM_SPLITS = int(n)
@@ -185,7 +186,8 @@ def _dense(q, k_cache, v_cache, cache_lens, start_k_offsets, num_splits, *, q_sc
         if k_cache.dim() != 4:
             raise ValueError("k_cache must be [batch, num_kv_heads, max_seqlen, head_dim]")
         S = k_cache.shape[2]
-        chunk_tokens = max(32, -(-math.ceil(S / num_splits) // 32) * 32)
+        # at least num_splits parts per sequence: chunks of at most this size
+        chunk_tokens = -max(32, -(-math.ceil(S / num_splits) // 32) * 32)
     return nat.ext().dense(q, k_cache, v_cache, cache_lens, start_k_offsets, s_aux, _scale_tensor(q_scale, q),
                            _scale_tensor(k_scale, q), _scale_tensor(v_scale, q), _out_code(out_dtype),
                            _sink_mode(sink_mode), _sm(sm_scale), int(chunk_tokens), _stream(q))

@@ -78,8 +78,11 @@ FSK_API int fsk_version(void);
  *              paged  -> block_table width (max blocks per sequence);
  *              dense  -> S_max (dim 2 of the cache).
  *   page_size: paged layout only (ignored otherwise).
- *   chunk_tokens: split size in tokens (multiple of 32) or 0 for the default
- *              the library would pick for this shape.
+ *   chunk_tokens: a multiple of 32: > 0 a fixed split size in tokens, 0 the
+ *              split the library picks for this shape, < 0 that automatic
+ *              split with chunks of at most -chunk_tokens tokens (the dense
+ *              entry points' split-count hint).  The decode entry points take
+ *              the same values.
  * Returns the byte count (> 0) or a negative status. */
 FSK_API int64_t fsk_workspace_bytes(int layout, int batch, int num_q_heads, int num_kv_heads,
                             int head_dim, int64_t kv_extent, int page_size,
@@ -169,7 +172,7 @@ FSK_API int fsk_decode_paged_noalloc(const void *q, int64_t q_stride_b, int64_t 
  * scores: [B, Hq, score_blocks] contiguous, in out_dtype; blocks past
  * score_blocks are not stored.  The workspace must hold
  * fsk_workspace_bytes(...) + fsk_score_workspace_bytes(B, Hq, score_blocks)
- * bytes, and a fixed chunk_tokens must be a multiple of 128.  Other
+ * bytes, and a nonzero chunk_tokens must be a multiple of 128.  Other
  * arguments as fsk_decode_varlen / fsk_decode_paged. */
 FSK_API int64_t fsk_score_workspace_bytes(int batch, int num_q_heads, int score_blocks);
 FSK_API int fsk_decode_varlen_scores(const void *q, int64_t q_stride_b, int64_t q_stride_h,

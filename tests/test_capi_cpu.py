@@ -370,3 +370,14 @@ def test_torch_binding_loads_with_the_library():
             nat.load().fsk_workspace_bytes(1, 1, 8, 8, 128, 1 << 16, 16, 33 * 32)
     finally:
         nat.set_option("chunk_tokens", 0)
+
+
+def test_workspace_bytes_with_a_chunk_cap(lib):
+    """A negative chunk_tokens caps the automatic split's chunk size (the
+    dense split-count hint): finer splits need at least the automatic
+    split's workspace; the cap must be a multiple of 32."""
+    for layout, extent in ((nat.FSK_LAYOUT_PAGED, 2048), (nat.FSK_LAYOUT_DENSE, 32768), (nat.FSK_LAYOUT_VARLEN, 131072)):
+        auto = lib.fsk_workspace_bytes(layout, 4, 32, 8, 128, extent, 16, 0)
+        for cap in (-32, -96, -512, -4096, -8192):
+            assert lib.fsk_workspace_bytes(layout, 4, 32, 8, 128, extent, 16, cap) >= auto > 0, (layout, cap)
+        assert lib.fsk_workspace_bytes(layout, 4, 32, 8, 128, extent, 16, -48) == nat.FSK_ERR_INVALID

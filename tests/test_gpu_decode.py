@@ -148,10 +148,19 @@ def test_paged_edge_lengths(lens):
         run_and_check(wl, what=f"lens {lens}")
 
 
-@pytest.mark.parametrize("chunk", [32, 64, 96, 128, 512])
+@pytest.mark.parametrize("chunk", [32, 64, 96, 128, 512, -32, -96, -256, -1024])
 def test_paged_chunk_sizes(chunk):
+    """Fixed splits (chunk_tokens > 0) and automatic ones with a chunk-size
+    cap (< 0)."""
     wl = W.make("C3", overrides=dict(B=3, lens=("list", [33, 700, 2049])), seed=3)
     run_and_check(wl, chunk_tokens=chunk, what=f"chunk {chunk}")
+
+
+@pytest.mark.parametrize("chunk", [-64, -512])
+def test_varlen_chunk_caps_at_full_size(chunk):
+    """C2 (4 x 32768 tokens, sinks) with chunks capped below the automatic
+    1024-token split: more, smaller splits of the same stream."""
+    run_and_check(W.make("C2"), chunk_tokens=chunk, what=f"C2 chunk cap {-chunk}")
 
 
 @pytest.fixture

@@ -25,9 +25,11 @@ def cdiv(a, b):
     return -(-a // b)
 
 
-def host_policy(total, B, NH, cus, fixed=0, skew=3):
+def host_policy(total, B, NH, cus, fixed=0, skew=3, most=0):
     """(chunk_min, chunk_max, target_units, u_max, xcd_skew) as the host sets
-    them for a stream of `total` padded tokens (stream bound total + 128 B)."""
+    them for a stream of `total` padded tokens (stream bound total + 128 B);
+    `most` > 0: an automatic split of chunks of at most `most` tokens (a
+    negative chunk_tokens)."""
     bound = total + 128 * B
 
     def unit_bound(c):
@@ -35,12 +37,14 @@ def host_policy(total, B, NH, cus, fixed=0, skew=3):
 
     if fixed:
         return fixed, fixed, 1, unit_bound(fixed), 0
+    cmax = min(most, CHUNK_MAX) if most else CHUNK_MAX
+    cmin = CHUNK_MIN if cmax >= CHUNK_MIN else min(SHORT_CHUNK, cmax)
     target = max(1, cus * 4 // NH)
     cap = max(4 * target, 256)
-    u_plan = unit_bound(CHUNK_MIN)
+    u_plan = unit_bound(cmin)
     if bound < target * CHUNK_MIN:
         u_plan = max(u_plan, min(unit_bound(SHORT_CHUNK), 33 * B + 1))
-    return CHUNK_MIN, CHUNK_MAX, target, max(unit_bound(CHUNK_MAX), min(u_plan, cap)), skew
+    return cmin, cmax, target, max(unit_bound(cmax), min(u_plan, cap)), skew
 
 
 def split(total, cmin, cmax, target, u_max, B, skew, NH, align):
@@ -144,6 +148,38 @@ def test_split_short_streams(total, B, want):
     assert (ce, co, paired) == (want, want, False) and n == cdiv(total, want)
     ce, *_ = split(total, *host_policy(total, B, 8, 256)[:4], B, 3, 8, 128)
     assert ce == 128
+
+
+@pytest.mark.parametrize("most", [32, 64, 96, 512, 1024, 4096])
+@pytest.mark.parametrize("total,B", [(4096, 4), (131072, 4), (131072, 1), (297_167, 32), (2_000_000, 16)])
+def test_split_chunk_size_caps(most, total, B):
+    """Automatic splits with a chunk-size cap (negative chunk_tokens, the
+    dense split-count hint): chunks never exceed the cap, the usual
+    invariants hold, and a capped split has at least as many chunks as
+    cdiv(total, cap) and as the uncapped one."""
+    for align in (32, 128):
+        if most % align:
+            continue
+        total_a = cdiv(total, align) * align
+        pol = host_policy(total_a, B, 8, 256, most=most)
+        ce, co, n, *_ = split(total_a, *pol[:4], B, pol[4], 8, align)
+        assert max(ce, co) <= most and n >= cdiv(total_a, most)
+        n_auto = split(total_a, *host_policy(total_a, B, 8, 256)[:4], B, 3, 8, align)[2]
+        assert n >= n_auto or max(ce, co) < most
+        check_case_policy(total_a, B, 8, pol, align)
+
+
+def check_case_policy(total, B, NH, pol, align):
+    cmin, cmax, target, u_max, skew = pol
+    ce, co, n, paired, starts, ic, isl, tok = split(total, cmin, cmax, target, u_max, B, skew, NH, align)
+    assert ce % align == 0 and co % align == 0 and co >= align and ce <= cmax
+    lens = np.where(np.arange(n) % 2 == 0, ce, co)
+    if n:
+        assert starts[0] == 0 and np.array_equal(starts[1:], np.cumsum(lens)[:-1])
+        assert starts[-1] + lens[-1] >= total
+    assert np.array_equal(tok, np.searchsorted(starts, np.arange(total), side="right") - 1)
+    assert n + B + 1 <= u_max
+    assert len(np.unique(ic.astype(np.int64) * NH + isl)) == n * NH
 
 
 def test_split_random_policies():
