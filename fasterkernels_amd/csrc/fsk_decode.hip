@@ -482,17 +482,21 @@ __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32
   seq_range_first<kLayout>(p, lane, start0, len0);
   start0_out = start0;
   len0_out = len0;
-  auto length = [&](int b0, int b) {
-    int len = len0;
-    if (b0 > 0) {
-      len = 0;
-      if (b < p.B) {
-        int start;
-        seq_range<kLayout>(p, b, start, len);
-      }
+  // The lengths of sequences 64 and up go to the pre[] table first (which
+  // the unit prefix overwrites below, each entry after its own lane has read
+  // it), four blocks of 64 per memory round trip rather than one.
+  for (int b0 = kWave; b0 < p.B; b0 += 4 * kWave) {
+    int l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int s;
+      seq_range_first<kLayout>(p, b0 + i * kWave + lane, s, l[i]);
     }
-    return b < p.B ? len : 0;
-  };
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (b0 + i * kWave + lane < p.B) pre[b0 + i * kWave + lane] = l[i];
+  }
+  auto length = [&](int b0, int b) { return b0 == 0 ? len0 : b < p.B ? pre[b] : 0; };
   // Stream length (the host bounds it below 2^31 - 4096, so the split
   // arithmetic is unsigned 32-bit: the plan sits on every workgroup's
   // critical path, and 64-bit division is a long software sequence).
