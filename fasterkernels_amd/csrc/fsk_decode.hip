@@ -1328,22 +1328,27 @@ struct ReduceParams {
 
 constexpr int kReduceThreads = 256;
 
-template <int D, int kOut>
+template <int D, int kOut, int kRows>
 __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) {
-  // One workgroup per (query head, sequence).  Thread t owns the float4
-  // column d4 = t % (D/4) of unit group grp = t / (D/4); group grp merges
-  // units grp, grp + kGroups, ... with an online LSE update, loading kPer
-  // units per round trip, and the groups combine through LDS.
+  // One workgroup per kRows query heads of a sequence (kRows > 1 for large
+  // batches of short sequences, whose rows have few partials each).  Thread
+  // t of row r = t / (256 / kRows) owns the float4 column d4 = t % (D/4) of
+  // unit group grp; group grp merges units grp, grp + kGroups, ... with an
+  // online LSE update, loading kPer units per round trip, and the groups
+  // combine through LDS.
   constexpr int kD4 = D / 4;
-  constexpr int kGroups = kReduceThreads / kD4;
+  constexpr int kRowThreads = kReduceThreads / kRows;
+  constexpr int kGroups = kRowThreads / kD4;
+  static_assert(kGroups >= 1, "a row needs at least one group of D/4 threads");
   constexpr int kPer = 4;
-  __shared__ float s_m[kGroups];
-  __shared__ float s_l[kGroups];
-  __shared__ f32x4 s_acc[kGroups][kD4];
+  __shared__ float s_m[kRows][kGroups];
+  __shared__ float s_l[kRows][kGroups];
+  __shared__ f32x4 s_acc[kRows][kGroups][kD4];
   const int tid = threadIdx.x;
-  const int d4 = tid % kD4;
-  const int grp = tid / kD4;
-  const int h = blockIdx.x;
+  const int row = tid / kRowThreads;
+  const int d4 = (tid - row * kRowThreads) % kD4;
+  const int grp = (tid - row * kRowThreads) / kD4;
+  const int h = blockIdx.x * kRows + row;
   const int b = blockIdx.y;
   const int kvh = h / p.G;
   const int hg = h - kvh * p.G;
@@ -1360,7 +1365,7 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) 
   // scores once the denominator is known.
   constexpr int kScorePre = 4;
   float bmax[kScorePre];
-  if (p.scores) {
+  if (kRows == 1 && p.scores) {
     const float* src = p.blk_max + ((int64_t)b * p.Hq + h) * p.nblk;
 #pragma unroll
     for (int i = 0; i < kScorePre; ++i) {
@@ -1401,22 +1406,23 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) 
     }
     m_t = mx;
   }
-  if (d4 == 0) s_m[grp] = m_t;
+  if (d4 == 0) s_m[row][grp] = m_t;
   __syncthreads();
-  float M = s_m[0];
+  float M = s_m[row][0];
 #pragma unroll
-  for (int q = 1; q < kGroups; ++q) M = fmaxf(M, s_m[q]);
+  for (int q = 1; q < kGroups; ++q) M = fmaxf(M, s_m[row][q]);
   const float M_use = (M == -INFINITY) ? 0.f : M;
   const float f = __builtin_amdgcn_exp2f(m_t - M_use);
-  s_acc[grp][d4] = a_t * f;
-  if (d4 == 0) s_l[grp] = l_t * f;
+  s_acc[row][grp][d4] = a_t * f;
+  if (d4 == 0) s_l[row][grp] = l_t * f;
   __syncthreads();
   // The denominator (every thread when block scores need it), then the
   // numerator (group 0, which stores the output row).
-  if (grp != 0 && !p.scores) return;
-  float den = s_l[0];
+  const bool scores = kRows == 1 && p.scores;
+  if (grp != 0 && !scores) return;
+  float den = s_l[row][0];
 #pragma unroll
-  for (int q = 1; q < kGroups; ++q) den += s_l[q];
+  for (int q = 1; q < kGroups; ++q) den += s_l[row][q];
   float fs = 1.f;     // scale of the numerator for an exp sink
   float ref = M_use;  // reference point of den
   if (p.s_aux) {
@@ -1434,7 +1440,7 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) 
     }
   }
 
-  if (p.scores) {
+  if (scores) {
     const int nvalid = (len_b + kScoreBlock - 1) / kScoreBlock;
     const float inv = 1.f / den;
     const float* src = p.blk_max + ((int64_t)b * p.Hq + h) * p.nblk;
@@ -1453,9 +1459,9 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(ReduceParams p) 
     for (int j = tid + kScorePre * kReduceThreads; j < p.nblk; j += kReduceThreads) put(j, src[j]);
   }
   if (grp != 0) return;
-  f32x4 num = s_acc[0][d4];
+  f32x4 num = s_acc[row][0][d4];
 #pragma unroll
-  for (int q = 1; q < kGroups; ++q) num += s_acc[q][d4];
+  for (int q = 1; q < kGroups; ++q) num += s_acc[row][q][d4];
   if (p.s_aux && p.sink_mode == FSK_SINK_EXP) num *= fs;
 
   uint8_t* o = p.out + (int64_t)b * p.o_sb + (int64_t)h * p.o_sh;
@@ -2030,13 +2036,22 @@ int dispatch_layout(int layout, bool scores, const Params& p, int grid, int q_dt
   return dispatch_qkv<D, kDense, false>(p, grid, q_dt, kv_dt, s);
 }
 
-template <int D>
-void launch_reduce(const ReduceParams& rp, int B, int o_dt, const Launch& s) {
-  dim3 grid(rp.Hq, B);
+template <int D, int kRows>
+void launch_reduce_rows(const ReduceParams& rp, int B, int o_dt, const Launch& s) {
+  dim3 grid(rp.Hq / kRows, B);
   dim3 block(kReduceThreads);
-  if (o_dt == FSK_F16) launch(reduce_kernel<D, kF16>, grid, block, 0, s, rp);
-  else if (o_dt == FSK_BF16) launch(reduce_kernel<D, kBF16>, grid, block, 0, s, rp);
-  else launch(reduce_kernel<D, kF32>, grid, block, 0, s, rp);
+  if (o_dt == FSK_F16) launch(reduce_kernel<D, kF16, kRows>, grid, block, 0, s, rp);
+  else if (o_dt == FSK_BF16) launch(reduce_kernel<D, kBF16, kRows>, grid, block, 0, s, rp);
+  else launch(reduce_kernel<D, kF32, kRows>, grid, block, 0, s, rp);
+}
+
+// Four query heads per workgroup when the batch has at least twice as many
+// sequences as the split has chunks (a few partials per row): a quarter of
+// the workgroups, each merging 8 units per round trip and row (D = 128).
+template <int D>
+void launch_reduce(const ReduceParams& rp, int B, int o_dt, bool rows4, const Launch& s) {
+  if (rows4 && rp.Hq % 4 == 0 && !rp.scores) launch_reduce_rows<D, 4>(rp, B, o_dt, s);
+  else launch_reduce_rows<D, 1>(rp, B, o_dt, s);
 }
 
 FastDiv make_fastdiv(uint32_t d) {
@@ -2145,9 +2160,10 @@ int run_decode(const Common& c) {
   rp.Hq = c.Hq; rp.Hkv = c.Hkv; rp.G = G;
   rp.blk_max = p.blk_max; rp.lens = p.lens_out; rp.scores = (uint8_t*)c.scores; rp.nblk = c.nblk;
   const Launch lr{c.stream, nullptr, ev[2]};
-  if (c.D == 64) launch_reduce<64>(rp, c.B, c.o_dt, lr);
-  else if (c.D == 128) launch_reduce<128>(rp, c.B, c.o_dt, lr);
-  else launch_reduce<256>(rp, c.B, c.o_dt, lr);
+  const bool rows4 = sp.chunk_min != sp.chunk_max && (int64_t)c.B >= 2 * (int64_t)sp.target_units;
+  if (c.D == 64) launch_reduce<64>(rp, c.B, c.o_dt, rows4, lr);
+  else if (c.D == 128) launch_reduce<128>(rp, c.B, c.o_dt, rows4, lr);
+  else launch_reduce<256>(rp, c.B, c.o_dt, rows4, lr);
   timing_keep(ev, true);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(FSK_ERR_HIP, std::string("kernel launch failed: ") + hipGetErrorString(e));

@@ -660,6 +660,20 @@ def test_batches_at_one_wave_with_empty_runs(layout, B):
     run_and_check(wl, chunk_tokens=32, what=f"{layout} B={B} chunk 32")
 
 
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("mode", ["exp", "linear"])
+def test_large_batch_reduce_rows(D, mode):
+    """Batches of at least twice as many sequences as the split has chunks
+    merge four query heads per reduce workgroup: 300 short sequences (some
+    empty), sinks in both folds, every head dim."""
+    r = np.random.default_rng(D)
+    lens = [int(x) for x in r.integers(0, 400, 300)]
+    wl = W.make("C3", overrides=dict(B=300, D=D, lens=("list", lens), sinks=True), seed=D)
+    if mode == "linear":
+        wl.s_aux = wl.s_aux.abs() + 0.5   # positive sinks: no cancellation in the linear fold
+    run_and_check(wl, sink_mode=mode, what=f"B=300 D={D} {mode}")
+
+
 @pytest.mark.parametrize("layout", ["varlen", "paged"])
 def test_maximum_batch(layout):
     """The largest batch the library takes (16384 sequences): the plan keeps
