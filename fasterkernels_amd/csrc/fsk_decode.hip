@@ -238,6 +238,7 @@ struct Params {
   FastDiv nh_div;          // divisor n_items_h
   int pair;                // varlen, head_dim 64: a wave takes KV heads 2i and 2i+1 as one 128-wide row
   int chunk_min, chunk_max;  // split size bounds in tokens (multiples of 32)
+  int chunk_pref;          // automatic split: the chunk count doubles while chunks would exceed this
   int target_units;        // preferred number of sequence chunks per call
   int u_max;               // workspace capacity in units
   int xcd_skew;            // automatic split: long/short chunk pairs for even/odd XCDs, in % (0: equal)
@@ -321,8 +322,9 @@ __device__ __forceinline__ HalfTile half_tile(const Params& p, int b, int start,
 // a sequence boundary carries that many fewer tokens in exchange.
 //
 // The chunk c is the larger of
-//   * stream / target (target = target_units, doubled while the chunk would
-//     exceed chunk_max: enough equal chunks to fill the GPU evenly), and
+//   * stream / target (target = target_units, doubled once if the chunk
+//     would exceed chunk_pref, then while it would exceed chunk_max: enough
+//     equal chunks to fill the GPU evenly), and
 //   * stream / (u_max - B - 1) (so every partial fits the workspace: a batch
 //     has at most n_chunks + B partials),
 // rounded to kAlign and clamped to [chunk_min, chunk_max]; the host sizes
@@ -382,6 +384,7 @@ constexpr int kShortChunk = 64;     // smallest automatic split of a short strea
 // (fsk_debug_split).
 struct SplitArgs {
   int chunk_min, chunk_max;  // split size bounds in tokens (multiples of align)
+  int chunk_pref;            // chunk_min <= chunk_pref <= chunk_max: see the doublings below
   int target_units;          // preferred number of chunks
   int u_max, B;              // workspace capacity in partials, sequences
   int xcd_skew;              // percent, 0: equal chunks
@@ -393,13 +396,15 @@ __host__ __device__ __forceinline__ Split split_geometry(uint32_t total, const S
   auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
   auto umin = [](uint32_t x, uint32_t y) { return x < y ? x : y; };
   const uint32_t align = (uint32_t)a.align;
-  // Chunks per call: target_units, doubled while that would need chunks above
-  // chunk_max (a batch too long for target_units full-size chunks gets twice
-  // as many chunks rather than a count that leaves some CUs one item short).
-  // cdiv(total, t) > chunk_max exactly when t < cdiv(total, chunk_max).
+  // Chunks per call: target_units, doubled once if that would need chunks
+  // above chunk_pref, then doubled while it would need chunks above
+  // chunk_max (a batch too long for target_units chunks gets twice as many
+  // rather than a count that leaves some CUs one item short).
+  // cdiv(total, t) > c exactly when t < cdiv(total, c).
   const uint32_t chunk_max = (uint32_t)a.chunk_max;
   const uint32_t t_need = cdiv(total, chunk_max);
   uint32_t target = (uint32_t)a.target_units;
+  if (target < cdiv(total, (uint32_t)a.chunk_pref)) target *= 2;
   while (target < t_need && target < (1u << 24)) target *= 2;
   auto up = [&](uint32_t x) { return (x + align - 1) / align * align; };
   uint32_t want = cdiv(total, target);
@@ -515,7 +520,7 @@ __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32
   }
   total = (uint32_t)uniform((int)total);
   nonempty = uniform(nonempty);
-  const SplitArgs sa{p.chunk_min, p.chunk_max, p.target_units, p.u_max, p.B, p.xcd_skew, p.n_items_h, kAlign};
+  const SplitArgs sa{p.chunk_min, p.chunk_max, p.chunk_pref, p.target_units, p.u_max, p.B, p.xcd_skew, p.n_items_h, kAlign};
   Split sp = split_geometry(total, sa);
   // Lead-ins where sequence boundaries are common and fall anywhere: lengths
   // that differ, at most 8 chunks per sequence.  Then many items hold a
@@ -1720,6 +1725,7 @@ struct Options {
   int waves_per_cu = 8;         // largest persistent grid (workgroups per CU)
   int target_waves_per_cu = 4;  // automatic split: units of work per CU
   int xcd_skew = 3;             // automatic split: extra share of the even XCDs, in % (see item_of)
+  int chunk_pref = 2432;        // automatic split: longest chunk before one doubling of the count (16-bit tokens)
   int qk_engine = 0;            // 0: QK and PV on the matrix cores; 1: the VALU tile (A/B measurement)
   int head_pairs = 1;           // varlen, head_dim 64: neighbouring KV heads as one 128-wide row (see pair_shape)
   int seg_tokens = 96;          // lead-in per sequence in the work stream where boundaries are common (tokens)
@@ -1820,12 +1826,13 @@ int64_t unit_bound(int layout, int B, int64_t kv_extent, int page_size, int chun
 }
 
 // Chunks the device can plan for a stream of at most `stream` tokens: a
-// split never has more than its target count of chunks (doubled while the
-// chunks would exceed chunk_max, as split_geometry does; a longer bound
-// doubles at least as often), plus one from an XCD-skewed split's even
-// count.
-int64_t chunk_bound(int64_t target_units, int chunk_max, int64_t stream) {
+// split never has more than its target count of chunks (doubled once past
+// chunk_pref and then while the chunks would exceed chunk_max, as
+// split_geometry does; a longer bound doubles at least as often), plus one
+// from an XCD-skewed split's even count.
+int64_t chunk_bound(int64_t target_units, int chunk_pref, int chunk_max, int64_t stream) {
   int64_t t = target_units;
+  if (t < cdiv(stream, chunk_pref)) t *= 2;
   const int64_t need = cdiv(stream, chunk_max);
   while (t < need && t < ((int64_t)1 << 24)) t *= 2;
   return t + 1;
@@ -1833,16 +1840,17 @@ int64_t chunk_bound(int64_t target_units, int chunk_max, int64_t stream) {
 
 // Split policy of one call: a fixed split when the caller (or the
 // chunk_tokens option) asks for one, else bounds for the device-side choice
-// and a workspace capacity that always holds the chunk_max split.
+// and a workspace capacity that always holds the chunk_pref split.
 struct SplitPlan {
-  int chunk_min, chunk_max, target_units;
+  int chunk_min, chunk_max, chunk_pref, target_units;
   int64_t u_max;
 };
-SplitPlan plan_split(int layout, int B, int64_t nh, int64_t kv_extent, int page_size, int chunk_tokens, int cus) {
+SplitPlan plan_split(int layout, int B, int64_t nh, int64_t kv_extent, int page_size, int chunk_tokens, int cus,
+                     int kv_bytes) {
   SplitPlan sp;
   const int fixed = chunk_tokens > 0 ? chunk_tokens : chunk_tokens == 0 ? g_opt.chunk_tokens : 0;
   if (fixed > 0) {
-    sp.chunk_min = sp.chunk_max = fixed;
+    sp.chunk_min = sp.chunk_max = sp.chunk_pref = fixed;
     sp.target_units = 1;
     sp.u_max = unit_bound(layout, B, kv_extent, page_size, fixed);
     return sp;
@@ -1853,6 +1861,13 @@ SplitPlan plan_split(int layout, int B, int64_t nh, int64_t kv_extent, int page_
   // makes a split coarser than the uncapped choice)
   sp.chunk_max = chunk_tokens < 0 && chunk_tokens > -kChunkMax ? -chunk_tokens : kChunkMax;
   sp.chunk_min = sp.chunk_max >= kChunkMin ? kChunkMin : std::min(kShortChunk, sp.chunk_max);
+  // Chunks longer than chunk_pref 16-bit tokens' worth of KV bytes are split
+  // once, up to one item per wave of a grid of 8 per CU (head_dim 128, 8 KV
+  // heads, B x 4096 tokens: B=80, 96, 128 from 217, 258, 345 us in the partial
+  // kernel to 206, 245, 321 us; C3's 2351-token chunks stay: halving them cost
+  // 3-4 us, as did halving the 2560-3200-token chunks of B=160, 200 x 4096 again).
+  const int pref = g_opt.chunk_pref * 2 / kv_bytes / 128 * 128;
+  sp.chunk_pref = std::max(sp.chunk_min, std::min(sp.chunk_max, pref));
   const int64_t target = std::max<int64_t>(1, (int64_t)cus * g_opt.target_waves_per_cu / nh);
   sp.target_units = (int)std::min<int64_t>(target, 1 << 20);
   const int64_t cap = std::max<int64_t>(4 * target, 256);
@@ -1863,7 +1878,12 @@ SplitPlan plan_split(int layout, int B, int64_t nh, int64_t kv_extent, int page_
   if (stream_bound(layout, B, kv_extent, page_size) < target * kChunkMin)
     u_plan = std::max(u_plan, std::min(unit_bound(layout, B, kv_extent, page_size, kShortChunk),
                                        33 * (int64_t)B + 1));
-  sp.u_max = std::max(unit_bound(layout, B, kv_extent, page_size, sp.chunk_max), std::min(u_plan, cap));
+  // The workspace holds every split the doubling can reach (at most
+  // chunk_bound chunks, plus one partial per sequence boundary), so that its
+  // capacity never makes the chunk count uneven over the grid.
+  const int64_t u_split =
+      chunk_bound(sp.target_units, sp.chunk_pref, sp.chunk_max, stream_bound(layout, B, kv_extent, page_size)) + B + 1;
+  sp.u_max = std::max(u_split, std::min(u_plan, cap));
   return sp;
 }
 
@@ -2070,7 +2090,7 @@ int run_decode(const Common& c) {
   const int cus = device_cus();
   if (c.chunk % 32 != 0) return fail(FSK_ERR_INVALID, "chunk_tokens must be a multiple of 32");
   const SplitPlan sp = plan_split(c.layout, c.B, plan_heads(c.layout, c.D, c.Hkv, G), c.kv_extent, c.page_size,
-                                  c.chunk, cus);
+                                  c.chunk, cus, elem_bytes(c.kv_dt));
   const bool pair =
       g_opt.head_pairs && pair_shape(c.layout, c.D, c.Hkv, G) && !c.scores && c.k_sh == 64 && c.v_sh == 64;
   if (c.layout == FSK_LAYOUT_PAGED && sp.chunk_max > kChunkMax)
@@ -2103,7 +2123,8 @@ int run_decode(const Common& c) {
   p.pair = pair ? 1 : 0;
   p.n_items_h = pair ? c.Hkv / 2 : c.Hkv * n_hb;
   p.nh_div = make_fastdiv((uint32_t)p.n_items_h);
-  p.chunk_min = sp.chunk_min; p.chunk_max = sp.chunk_max; p.target_units = sp.target_units;
+  p.chunk_min = sp.chunk_min; p.chunk_max = sp.chunk_max; p.chunk_pref = sp.chunk_pref;
+  p.target_units = sp.target_units;
   // The skew is not applied to a fixed split, nor at head_dim 256: there the
   // even and odd XCDs stream at the same rate (16-bit KV: partial kernel
   // 3-4 % slower with it, paged and varlen; e4m3: no difference).
@@ -2131,7 +2152,7 @@ int run_decode(const Common& c) {
   // C4's decode step ~0.25 µs longer; the other configs were unchanged).
   const int64_t w_max =
       std::min<int64_t>(u_max * c.Hkv * n_hb,
-                        chunk_bound(sp.target_units, sp.chunk_max,
+                        chunk_bound(sp.target_units, sp.chunk_pref, sp.chunk_max,
                                     stream_bound(c.layout, c.B, c.kv_extent, p.page_size)) * p.n_items_h);
   const int64_t grid64 = std::min<int64_t>(w_max, (int64_t)cus * g_opt.waves_per_cu);
   const int grid = (int)std::max<int64_t>(grid64, 1);
@@ -2304,6 +2325,12 @@ int fsk_set_option(const char* name, int64_t value) {
     g_opt.qk_engine = (int)value;
     return FSK_OK;
   }
+  if (!strcmp(name, "chunk_pref")) {
+    if (value < kChunkMin || value > kChunkMax || value % 128)
+      return fail(FSK_ERR_INVALID, "chunk_pref must be a multiple of 128 in [128, 4096]");
+    g_opt.chunk_pref = (int)value;
+    return FSK_OK;
+  }
   if (!strcmp(name, "xcd_skew")) {
     if (value < 0 || value > 50) return fail(FSK_ERR_INVALID, "xcd_skew in [0, 50]");
     g_opt.xcd_skew = (int)value;
@@ -2365,8 +2392,9 @@ int64_t fsk_workspace_bytes(int layout, int batch, int num_q_heads, int num_kv_h
   if (chunk_tokens % 32) return fail(FSK_ERR_INVALID, "chunk_tokens: a multiple of 32");
   const int G = num_q_heads / num_kv_heads;
   const int B = batch > 0 ? batch : 1;
+  // sized for 16-bit KV: the smallest chunk_pref, so the most chunks
   const SplitPlan sp = plan_split(layout, B, plan_heads(layout, head_dim, num_kv_heads, G), kv_extent, page_size,
-                                  chunk_tokens, device_cus());
+                                  chunk_tokens, device_cus(), 2);
   const int64_t u_max = sp.u_max;
   return ws_layout(B, num_kv_heads, G, head_dim, u_max).total;
 }
@@ -2643,18 +2671,20 @@ int fsk_fp8_decode_table(uint16_t* out, void* stream) {
   return FSK_OK;
 }
 
-int fsk_debug_split(int64_t total, int chunk_min, int chunk_max, int target_units, int64_t u_max, int batch,
-                    int xcd_skew, int head_slots, int align, int32_t* geometry, int32_t* chunk_start,
+int fsk_debug_split(int64_t total, int chunk_min, int chunk_max, int chunk_pref, int target_units, int64_t u_max,
+                    int batch, int xcd_skew, int head_slots, int align, int32_t* geometry, int32_t* chunk_start,
                     int32_t* item_chunk, int32_t* item_slot, int32_t* token_chunk) {
   if (!geometry) return fail(FSK_ERR_INVALID, "null geometry");
   if (total < 0 || total >= ((int64_t)1 << 31) - 4096) return fail(FSK_ERR_INVALID, "total out of range");
   if (align != 32 && align != 128) return fail(FSK_ERR_INVALID, "align must be 32 or 128");
   if (chunk_min < 32 || chunk_min % align || chunk_max < chunk_min || chunk_max % align || chunk_max > (1 << 24))
     return fail(FSK_ERR_INVALID, "chunk bounds must be multiples of align with 32 <= chunk_min <= chunk_max");
+  if (chunk_pref < chunk_min || chunk_pref > chunk_max)
+    return fail(FSK_ERR_INVALID, "chunk_pref must lie in [chunk_min, chunk_max]");
   if (target_units < 1 || u_max < 0 || u_max >= ((int64_t)1 << 31) || batch < 0 || xcd_skew < 0 || xcd_skew > 50 ||
       head_slots < 1 || head_slots > (1 << 16))
     return fail(FSK_ERR_INVALID, "bad split arguments");
-  const SplitArgs a{chunk_min, chunk_max, target_units, (int)u_max, batch, xcd_skew, head_slots, align};
+  const SplitArgs a{chunk_min, chunk_max, chunk_pref, target_units, (int)u_max, batch, xcd_skew, head_slots, align};
   const Split sp = split_geometry((uint32_t)total, a);
   geometry[0] = sp.c_e;
   geometry[1] = sp.c_o;

@@ -62,7 +62,7 @@ SIGNATURES = {
     "fsk_paged_write": (_I, [_P, _L, _L, _P, _L, _L, _P, _L, _P, _L, _L, _L, _P, _L, _L, _L, _I, _I,
                              _I, _I, _I, _I, _P, _P, _P, _L, _P, _L, _P]),
     "fsk_fp8_decode_table": (_I, [_P, _P]),
-    "fsk_debug_split": (_I, [_L, _I, _I, _I, _L, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
+    "fsk_debug_split": (_I, [_L, _I, _I, _I, _I, _L, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
     "fsk_enable_kernel_timing": (_I, [_I]),
     "fsk_kernel_timing": (_I, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
                                ctypes.POINTER(ctypes.c_int64)]),

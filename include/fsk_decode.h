@@ -280,8 +280,8 @@ FSK_API int fsk_fp8_decode_table(uint16_t *out, void *stream);
 /* Debug: the chunk geometry and work-item mapping of the decode kernels'
  * device-side plan, computed on the host by the same functions, for a stream
  * of `total` padded tokens (each sequence padded to `align` = 32, or 128 with
- * block scores).  chunk_min / chunk_max / target_units / u_max / xcd_skew are
- * the split policy a decode call passes to its kernel; head_slots = work items
+ * block scores).  chunk_min / chunk_max / chunk_pref / target_units / u_max /
+ * xcd_skew are the split policy a decode call passes to its kernel; head_slots = work items
  * per chunk.  geometry[0..3] = long chunk, short chunk (equal without an XCD
  * skew), chunk count n, XCD pairing flag.  Optional outputs (null to skip):
  * chunk_start[n]; item_chunk[n * head_slots] and item_slot[...] (the chunk
@@ -290,7 +290,8 @@ FSK_API int fsk_fp8_decode_table(uint16_t *out, void *stream);
  * split-KV partition (fskernels/triton/triton_gqa_decode_hf.py:52-54), with
  * the chunk count chosen for this GPU. */
 FSK_API int fsk_debug_split(int64_t total, int chunk_min, int chunk_max,
-                            int target_units, int64_t u_max, int batch,
+                            int chunk_pref, int target_units, int64_t u_max,
+                            int batch,
                             int xcd_skew, int head_slots, int align,
                             int32_t *geometry, int32_t *chunk_start,
                             int32_t *item_chunk, int32_t *item_slot,
@@ -305,6 +306,10 @@ FSK_API int fsk_debug_split(int64_t total, int chunk_min, int chunk_max,
  *   "xcd_skew"            automatic split: extra share of the even XCDs, in %
  *                         (0..50, default 3; 0 = equal chunks; not applied at
  *                         head_dim 256, nor to a fixed chunk_tokens split)
+ *   "chunk_pref"          automatic split: chunks longer than this many
+ *                         tokens of 16-bit KV (twice as many of e4m3) make
+ *                         the chunk count double once (multiple of 128 in
+ *                         128..4096, default 2432)
  *   "seg_tokens"          work-stream positions laid before each sequence when
  *                         non-empty lengths differ and there are at most 8
  *                         chunks per sequence, so that items holding a

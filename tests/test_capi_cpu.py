@@ -350,6 +350,23 @@ def test_xcd_skew_option(lib):
     assert lib.fsk_set_option(b"xcd_skew", 3) == nat.FSK_OK
 
 
+def test_chunk_pref_option(lib):
+    for bad in (0, 64, 200, 4224, 8192):
+        assert lib.fsk_set_option(b"chunk_pref", bad) == nat.FSK_ERR_INVALID, bad
+    assert lib.fsk_set_option(b"chunk_pref", 4096) == nat.FSK_OK
+    assert lib.fsk_set_option(b"chunk_pref", 2432) == nat.FSK_OK
+
+
+def test_workspace_holds_the_doubled_split(lib):
+    """A stream over 128 chunks of 2432 tokens (8 KV heads) plans 256
+    chunks: the workspace holds them, whatever chunk_pref says (the query
+    sizes for 16-bit KV, the smallest chunk ceiling)."""
+    cus = 256  # MI355X's CU count, and the library's count where no GPU is visible
+    per_unit = 8 * 4 * (128 + 2) * 4
+    need = nat.workspace_bytes(nat.FSK_LAYOUT_PAGED, 128, 32, 8, 128, 256, 16, 0)
+    assert need >= (2 * max(1, cus * 4 // 8) + 1 + 128 + 1) * per_unit
+
+
 def test_torch_binding_loads_with_the_library():
     """The torch binding is built next to the library, links that same file
     (one copy of the library's state: options, timing, last error) and

@@ -18,52 +18,63 @@ import pytest
 
 from fasterkernels_amd import native as nat
 
-CHUNK_MIN, CHUNK_MAX, SKEW_MIN, SHORT_CHUNK = 128, 4096, 512, 64
+CHUNK_MIN, CHUNK_MAX, SKEW_MIN, SHORT_CHUNK, CHUNK_PREF = 128, 4096, 512, 64, 2432
 
 
 def cdiv(a, b):
     return -(-a // b)
 
 
-def host_policy(total, B, NH, cus, fixed=0, skew=3, most=0):
-    """(chunk_min, chunk_max, target_units, u_max, xcd_skew) as the host sets
+def doubled_target(target, total, cpref, cmax):
+    """The chunk count bound of a split: doubled once past cpref, then while
+    chunks would exceed cmax."""
+    t = target * 2 if target < cdiv(total, cpref) else target
+    while t < cdiv(total, cmax) and t < (1 << 24):
+        t *= 2
+    return t
+
+
+def host_policy(total, B, NH, cus, fixed=0, skew=3, most=0, kv_bytes=2):
+    """(chunk_min, chunk_max, chunk_pref, target_units, u_max, xcd_skew) as the host sets
     them for a stream of `total` padded tokens (stream bound total + 128 B);
     `most` > 0: an automatic split of chunks of at most `most` tokens (a
-    negative chunk_tokens)."""
+    negative chunk_tokens); kv_bytes: bytes per KV element."""
     bound = total + 128 * B
 
     def unit_bound(c):
         return cdiv(bound, c) + B + 1
 
     if fixed:
-        return fixed, fixed, 1, unit_bound(fixed), 0
+        return fixed, fixed, fixed, 1, unit_bound(fixed), 0
     cmax = min(most, CHUNK_MAX) if most else CHUNK_MAX
     cmin = CHUNK_MIN if cmax >= CHUNK_MIN else min(SHORT_CHUNK, cmax)
+    cpref = max(cmin, min(cmax, CHUNK_PREF * 2 // kv_bytes // 128 * 128))
     target = max(1, cus * 4 // NH)
     cap = max(4 * target, 256)
     u_plan = unit_bound(cmin)
     if bound < target * CHUNK_MIN:
         u_plan = max(u_plan, min(unit_bound(SHORT_CHUNK), 33 * B + 1))
-    return cmin, cmax, target, max(unit_bound(cmax), min(u_plan, cap)), skew
+    t = doubled_target(target, bound, cpref, cmax)  # chunk_bound, less one
+    return cmin, cmax, cpref, target, max(t + 1 + B + 1, min(u_plan, cap)), skew
 
 
-def split(total, cmin, cmax, target, u_max, B, skew, NH, align):
+def split(total, cmin, cmax, cpref, target, u_max, B, skew, NH, align):
     lib = nat.load()
     geo = (ctypes.c_int32 * 4)()
-    nat.check(lib.fsk_debug_split(total, cmin, cmax, target, u_max, B, skew, NH, align, geo, None, None, None, None))
+    nat.check(lib.fsk_debug_split(total, cmin, cmax, cpref, target, u_max, B, skew, NH, align, geo, None, None, None, None))
     ce, co, n, paired = list(geo)
     starts = np.zeros(max(n, 1), np.int32)
     ic = np.zeros(max(n * NH, 1), np.int32)
     isl = np.zeros(max(n * NH, 1), np.int32)
     tok = np.zeros(max(total, 1), np.int32)
-    nat.check(lib.fsk_debug_split(total, cmin, cmax, target, u_max, B, skew, NH, align, geo,
+    nat.check(lib.fsk_debug_split(total, cmin, cmax, cpref, target, u_max, B, skew, NH, align, geo,
                                   starts.ctypes.data, ic.ctypes.data, isl.ctypes.data, tok.ctypes.data))
     return ce, co, n, bool(paired), starts[:n], ic[:n * NH], isl[:n * NH], tok[:total]
 
 
 def check_case(total, B, NH, cus, fixed, skew, align):
-    cmin, cmax, target, u_max, skew = host_policy(total, B, NH, cus, fixed, skew)
-    ce, co, n, paired, starts, ic, isl, tok = split(total, cmin, cmax, target, u_max, B, skew, NH, align)
+    cmin, cmax, cpref, target, u_max, skew = host_policy(total, B, NH, cus, fixed, skew)
+    ce, co, n, paired, starts, ic, isl, tok = split(total, cmin, cmax, cpref, target, u_max, B, skew, NH, align)
     what = f"total={total} B={B} NH={NH} cus={cus} fixed={fixed} skew={skew} align={align}: ce={ce} co={co} n={n}"
     # chunk sizes
     assert ce % align == 0 and co % align == 0 and co >= align and ce <= cmax, what
@@ -91,12 +102,10 @@ def check_case(total, B, NH, cus, fixed, skew, align):
     assert np.array_equal(tok, np.searchsorted(starts, x, side="right") - 1), what
     # every partial fits: at most n + B of them, and the workspace holds u_max
     assert n + B + 1 <= u_max, what
-    # at most the target count of chunks (doubled while chunks would exceed
-    # chunk_max) plus one: the host sizes the persistent grid on this bound
-    t = target
-    while t < cdiv(total, cmax) and t < (1 << 24):
-        t *= 2
-    assert n <= t + 1, what
+    # at most the target count of chunks (doubled once past chunk_pref, then
+    # while chunks would exceed chunk_max) plus one: the host sizes the
+    # persistent grid on this bound
+    assert n <= doubled_target(target, total, cpref, cmax) + 1, what
     # work items: a bijection onto (chunk, head slot), long chunks on even XCDs
     assert ((ic >= 0) & (ic < n) & (isl >= 0) & (isl < NH)).all(), what
     assert len(np.unique(ic.astype(np.int64) * NH + isl)) == n * NH, what
@@ -109,14 +118,16 @@ def test_split_rejects_bad_arguments():
     lib = nat.load()
     geo = (ctypes.c_int32 * 4)()
     bad = [
-        (-1, 128, 2048, 1, 100, 1, 0, 8, 32),
-        (100, 16, 2048, 1, 100, 1, 0, 8, 32),      # chunk_min below 32
-        (100, 128, 64, 1, 100, 1, 0, 8, 32),       # chunk_max below chunk_min
-        (100, 96, 2048, 1, 100, 1, 0, 8, 128),     # not a multiple of align
-        (100, 128, 2048, 0, 100, 1, 0, 8, 32),     # no target
-        (100, 128, 2048, 1, 100, 1, 0, 0, 32),     # no head slots
-        (100, 128, 2048, 1, 100, 1, 0, 8, 48),     # align
-        (100, 128, 2048, 1, 100, 1, 51, 8, 32),    # skew
+        (-1, 128, 2048, 2048, 1, 100, 1, 0, 8, 32),
+        (100, 16, 2048, 2048, 1, 100, 1, 0, 8, 32),      # chunk_min below 32
+        (100, 128, 64, 64, 1, 100, 1, 0, 8, 32),         # chunk_max below chunk_min
+        (100, 96, 2048, 2048, 1, 100, 1, 0, 8, 128),     # not a multiple of align
+        (100, 128, 2048, 64, 1, 100, 1, 0, 8, 32),       # chunk_pref below chunk_min
+        (100, 128, 2048, 4096, 1, 100, 1, 0, 8, 32),     # chunk_pref above chunk_max
+        (100, 128, 2048, 2048, 0, 100, 1, 0, 8, 32),     # no target
+        (100, 128, 2048, 2048, 1, 100, 1, 0, 0, 32),     # no head slots
+        (100, 128, 2048, 2048, 1, 100, 1, 0, 8, 48),     # align
+        (100, 128, 2048, 2048, 1, 100, 1, 51, 8, 32),    # skew
     ]
     for args in bad:
         assert lib.fsk_debug_split(*args, geo, None, None, None, None) == nat.FSK_ERR_INVALID, args
@@ -133,8 +144,22 @@ def test_split_headline_and_edge_streams(total, NH):
 def test_split_m0_geometry():
     """M0: 131072 tokens, 8 KV heads, 256 CUs -> 1056/992-token chunk pairs,
     128 chunks, the long ones on the even XCDs."""
-    ce, co, n, paired, *_ = split(131072, *host_policy(131072, 4, 8, 256)[:4], 4, 3, 8, 32)
+    ce, co, n, paired, *_ = split(131072, *host_policy(131072, 4, 8, 256)[:5], 4, 3, 8, 32)
     assert (ce, co, n, paired) == (1056, 992, 128, True)
+
+
+@pytest.mark.parametrize("total,B,kv_bytes,want", [
+    (524288, 128, 2, (2112, 1984, 256)), (507904, 124, 2, (2048, 1920, 256)), (393216, 96, 2, (1600, 1472, 256)),
+    (327680, 80, 2, (1344, 1216, 256)), (262144, 64, 2, (2112, 1984, 128)), (278528, 32, 2, (2272, 2080, 128)),
+    (300896, 32, 2, (2464, 2272, 128)), (655360, 160, 2, (2656, 2464, 256)), (819200, 200, 2, (3296, 3104, 256)), (393216, 96, 1, (3168, 2976, 128))])
+def test_split_long_streams(total, B, kv_bytes, want):
+    """Streams longer than 128 chunks of 2432 16-bit tokens (8 KV heads, 256
+    CUs) take twice as many chunks, once: B=128 x 4096 tokens gets 256 chunk
+    pairs of 2112/1984 tokens, not 128 of 4096; B=160 x 4096 keeps 256
+    chunks of 2560 rather than 512; e4m3 KV (1 byte) splits at twice the
+    tokens."""
+    ce, co, n, paired, *_ = split(total, *host_policy(total, B, 8, 256, kv_bytes=kv_bytes)[:5], B, 3, 8, 32)
+    assert (ce, co, n) == want and paired
 
 
 @pytest.mark.parametrize("total,B,want", [(5120, 4, 96), (4096, 4, 64), (2048, 4, 64), (8192, 4, 128),
@@ -144,9 +169,9 @@ def test_split_short_streams(total, B, want):
     take half as many chunks, of 64 to 128 tokens, while that averages at
     most 32 chunks per sequence; from 8192 tokens up the split is the plain
     128-token one.  Block scores (align 128) keep 128."""
-    ce, co, n, paired, *_ = split(total, *host_policy(total, B, 8, 256)[:4], B, 3, 8, 32)
+    ce, co, n, paired, *_ = split(total, *host_policy(total, B, 8, 256)[:5], B, 3, 8, 32)
     assert (ce, co, paired) == (want, want, False) and n == cdiv(total, want)
-    ce, *_ = split(total, *host_policy(total, B, 8, 256)[:4], B, 3, 8, 128)
+    ce, *_ = split(total, *host_policy(total, B, 8, 256)[:5], B, 3, 8, 128)
     assert ce == 128
 
 
@@ -162,16 +187,16 @@ def test_split_chunk_size_caps(most, total, B):
             continue
         total_a = cdiv(total, align) * align
         pol = host_policy(total_a, B, 8, 256, most=most)
-        ce, co, n, *_ = split(total_a, *pol[:4], B, pol[4], 8, align)
+        ce, co, n, *_ = split(total_a, *pol[:5], B, pol[5], 8, align)
         assert max(ce, co) <= most and n >= cdiv(total_a, most)
-        n_auto = split(total_a, *host_policy(total_a, B, 8, 256)[:4], B, 3, 8, align)[2]
+        n_auto = split(total_a, *host_policy(total_a, B, 8, 256)[:5], B, 3, 8, align)[2]
         assert n >= n_auto or max(ce, co) < most
         check_case_policy(total_a, B, 8, pol, align)
 
 
 def check_case_policy(total, B, NH, pol, align):
-    cmin, cmax, target, u_max, skew = pol
-    ce, co, n, paired, starts, ic, isl, tok = split(total, cmin, cmax, target, u_max, B, skew, NH, align)
+    cmin, cmax, cpref, target, u_max, skew = pol
+    ce, co, n, paired, starts, ic, isl, tok = split(total, cmin, cmax, cpref, target, u_max, B, skew, NH, align)
     assert ce % align == 0 and co % align == 0 and co >= align and ce <= cmax
     lens = np.where(np.arange(n) % 2 == 0, ce, co)
     if n:
