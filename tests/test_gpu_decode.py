@@ -674,6 +674,20 @@ def test_large_batch_reduce_rows(D, mode):
     run_and_check(wl, sink_mode=mode, what=f"B=300 D={D} {mode}")
 
 
+@pytest.mark.parametrize("chunk", [0, 32, 64, 128])
+def test_paged_large_batch_row_ends(chunk):
+    """Paged batches over 64 sequences load each segment's length together
+    with its page window, which the padded length bounds until then: lengths
+    at and near the end of an odd-length block-table row (33 pages of 16
+    tokens), empty and 1-token sequences, chunks that start inside padding."""
+    r = np.random.default_rng(61 + chunk)
+    edge = [0, 1, 15, 16, 17, 31, 32, 33, 511, 512, 513, 527, 528, 528, 0, 527]
+    lens = edge + [int(x) for x in r.integers(0, 529, 100 - len(edge))]
+    wl = W.make("C3", overrides=dict(B=100, lens=("list", lens), max_blocks=33, sinks=True), seed=62)
+    assert wl.block_table.shape[1] == 33
+    run_and_check(wl, chunk_tokens=chunk, what=f"B=100 max_blocks=33 chunk={chunk}")
+
+
 @pytest.mark.parametrize("layout", ["varlen", "paged"])
 def test_maximum_batch(layout):
     """The largest batch the library takes (16384 sequences): the plan keeps
