@@ -133,13 +133,17 @@ FSK_API int fsk_decode_paged(const void *q, int64_t q_stride_b, int64_t q_stride
  * callers that cannot allocate device memory (code under HIP-graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and
  * results as fsk_decode_paged, without workspace / workspace_bytes: the
- * workspace is a device array inside the library of
- * FSK_NOALLOC_SCRATCH_BYTES bytes per device, held from the first call on a
- * device until the process ends.  The call allocates nothing and frees
- * nothing.  It returns FSK_ERR_UNSUPPORTED, launching nothing, when the shape
- * needs more workspace than that (fsk_workspace_bytes(FSK_LAYOUT_PAGED, ...)
- * tells how much; the M0 shape, B=4 x 32768 tokens, Hq=32, Hkv=8, D=128,
- * needs 8.6 MB).  Every call on one device shares that device's array:
+ * workspace is a device array of FSK_NOALLOC_SCRATCH_BYTES bytes inside the
+ * library's GPU code object.  It is allocated with that code object, so every
+ * device on which any kernel of this library has been loaded holds it (also
+ * in processes that never call this entry point), until the process ends.
+ * The first call on a device looks up the array's address on that device
+ * (hipGetSymbolAddress) and keeps it; that call and all later ones may run
+ * under HIP-graph capture.  The call allocates nothing and frees nothing.
+ * It returns FSK_ERR_UNSUPPORTED, launching nothing, when the shape needs
+ * more workspace than that (fsk_workspace_bytes(FSK_LAYOUT_PAGED, ...) tells
+ * how much; the M0 shape, B=4 x 32768 tokens, Hq=32, Hkv=8, D=128, needs
+ * 8,519,936 bytes, 8.5 MB).  Every call on one device shares that device's array:
  * calls that overlap on one device (two streams, two threads, or two entries
  * of one graph that may run concurrently) race and give wrong results;
  * serialise them.  Nothing in the array needs to start at zero (each call

@@ -2,7 +2,8 @@
 workspace entry point (fsk_decode_paged), both called through the C ABI.
 
 The two run the same kernels with the same split plan, so their outputs must
-be bit-identical.  Two calls in a row, the second on a smaller batch with
+be bit-identical, eagerly and when the allocation-free call is replayed from a
+captured graph.  Two calls in a row, the second on a smaller batch with
 different data, check that nothing of the first call's scratch contents leaks
 into the second; a shape whose workspace exceeds the scratch is refused
 before any launch.
@@ -49,6 +50,51 @@ def both(wl):
     nat.check(lib.fsk_decode_paged_noalloc(*paged_args(wl, got), 0, stream))
     torch.cuda.synchronize()
     return ref, got
+
+
+def workspace_call(wl, out):
+    """The workspace entry point (fsk_decode_paged) into ``out``, eagerly."""
+    lib = nat.load()
+    P, Hkv, PS, D = wl.k.shape
+    nbytes = nat.workspace_bytes(nat.FSK_LAYOUT_PAGED, wl.B, wl.Hq, Hkv, D, wl.block_table.shape[1], PS, 0)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    nat.check(lib.fsk_decode_paged(*paged_args(wl, out), ws.data_ptr(), nbytes, 0, nat.stream_handle(DEV)))
+    torch.cuda.synchronize()
+
+
+def test_noalloc_captured_in_a_graph_with_its_first_call_inside():
+    """The allocation-free call captured into a HIP graph (torch.cuda.graph,
+    global capture mode), with the process's first call of that entry point
+    inside the capture: the scratch address lookup and the launches are
+    legal there.  Each replay, after eager work and a synchronisation that
+    give q and the sinks new values in place, is bit-identical to the
+    workspace entry point on the same inputs.  (This test comes first in the
+    file so that the captured call is the process's first.)"""
+    wl = W.make("C3", overrides=dict(B=5, lens=("list", [1, 40, 700, 3000, 9000]), sinks=True), seed=44).to(DEV)
+    lib = nat.load()
+    out = torch.full((wl.B, wl.Hq, wl.D), float("nan"), dtype=wl.out_dtype, device=DEV)
+    ref = torch.full_like(out, float("nan"))
+    workspace_call(wl, ref)  # (also loads the kernels before the capture)
+    print("noalloc: capturing the first allocation-free call of the process", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = lib.fsk_decode_paged_noalloc(*paged_args(wl, out), 0, nat.stream_handle(DEV))
+    assert st == nat.FSK_OK, lib.fsk_last_error()
+    torch.cuda.synchronize()
+    g = torch.Generator().manual_seed(45)
+    for r in range(4):
+        if r:
+            wl.q.copy_(torch.randn(wl.q.shape, generator=g).to(wl.q.dtype).to(DEV))
+            wl.s_aux.copy_(torch.randn(wl.s_aux.shape, generator=g).to(DEV))
+        workspace_call(wl, ref)
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        print(f"noalloc: replay {r}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(ref).all()
+        assert torch.equal(out, ref), f"replay {r}"
+    del graph
 
 
 def test_noalloc_matches_workspace_entry_on_consecutive_calls():
