@@ -291,7 +291,10 @@ at::Tensor dense(const at::Tensor& q_in, const at::Tensor& k_cache, const at::Te
   const at::Tensor lens = int32_contig(cache_lens, "cache_lens", dev);
   if (lens.numel() < B) raise(FSK_ERR_INVALID, "cache_lens must have one entry per sequence");
   c10::optional<at::Tensor> starts;
-  if (start_k_offsets && start_k_offsets->defined()) starts = int32_contig(*start_k_offsets, "start_k_offsets", dev);
+  if (start_k_offsets && start_k_offsets->defined()) {
+    starts = int32_contig(*start_k_offsets, "start_k_offsets", dev);
+    if (starts->numel() < B) raise(FSK_ERR_INVALID, "start_k_offsets must have one entry per sequence");
+  }
   const auto sk = sinks(s_aux, Hq, dev);
   const auto qs = scale(q_scale, "scale_q", dev), ks = scale(k_scale, "scale_k", dev);
   const auto vs = scale(v_scale, "scale_v", dev);

@@ -74,7 +74,7 @@ class PagedDecodeStep:
     def __init__(self, cache: PagedKVCache, layer_idx: int, seq_ids: Sequence[int], num_q_heads: int, *,
                  q_dtype: Optional[torch.dtype] = None, src_dtype: Optional[torch.dtype] = None,
                  out_dtype: Optional[torch.dtype] = None, s_aux: Optional[torch.Tensor] = None,
-                 sink_mode: str = "exp"):
+                 sink_mode: str = "linear"):
         cache._require_gpu()
         self.cache = cache
         self.layer = int(layer_idx)

@@ -144,7 +144,7 @@ def _sm(sm_scale):
 # varlen
 # ---------------------------------------------------------------------------
 def flash_decode_gqa_varlen(q, k_varlen, v_varlen, cu_seqlens_k, s_aux=None, *,
-                            sink_mode: str = "exp", k_scale=None, v_scale=None,
+                            sink_mode: str = "linear", k_scale=None, v_scale=None,
                             out_dtype: torch.dtype | None = None, sm_scale: float | None = None,
                             chunk_tokens: int = 0, return_block_scores: bool = False,
                             score_blocks: int | None = None):
@@ -154,9 +154,13 @@ def flash_decode_gqa_varlen(q, k_varlen, v_varlen, cu_seqlens_k, s_aux=None, *,
     CUDA/TileLang variants fskernels/cuda/cuda_fd_gqa.py:14-15,
     fskernels/tilelang/tilelang_gqa_decode.py:135-172).  q [B, Hq, D];
     k_varlen / v_varlen [T, Hkv, D] packed by cu_seqlens_k int32 [B+1];
-    s_aux fp32 [Hq] sinks folded per ``sink_mode`` ("exp": sink logit, the
-    reference tests' oracle; "linear": added to the denominator as the
-    reference kernels do).  Returns a new [B, Hq, D] tensor of q's dtype
+    s_aux fp32 [Hq] sinks folded per ``sink_mode``: "linear" (default) adds
+    the sink to the softmax denominator relative to the running maximum, as
+    all three replaced kernels do (triton_gqa_decode.py:112-115,
+    flash_decode_cuda.cu:151-153, tilelang_gqa_decode.py:117-120); "exp"
+    treats it as one more logit with a zero value row (the reference tests'
+    oracle, tests/test_triton_fd_gqa.py:27-33, and the sink-logit form of
+    models with attention sinks).  Returns a new [B, Hq, D] tensor of q's dtype
     (``out_dtype`` overrides it).  fp8 K/V need k_scale / v_scale.
 
     ``return_block_scores=True`` returns ``(out, S)`` with S [B, Hq, n] the
@@ -179,7 +183,7 @@ def flash_decode_gqa_varlen(q, k_varlen, v_varlen, cu_seqlens_k, s_aux=None, *,
 # dense (HF static cache)
 # ---------------------------------------------------------------------------
 def _dense(q, k_cache, v_cache, cache_lens, start_k_offsets, num_splits, *, q_scale=None,
-           k_scale=None, v_scale=None, out_dtype=None, s_aux=None, sink_mode="exp",
+           k_scale=None, v_scale=None, out_dtype=None, s_aux=None, sink_mode="linear",
            sm_scale=None, chunk_tokens=0):
     if not chunk_tokens and num_splits and num_splits > 1:
         _on_gpu(k_cache, "k_cache")
@@ -194,7 +198,7 @@ def _dense(q, k_cache, v_cache, cache_lens, start_k_offsets, num_splits, *, q_sc
 
 
 def flash_decode_gqa_hf_dense_optimized(q, k_cache, v_cache, cache_lens, start_k_offsets=None,
-                                        num_splits=None, *, s_aux=None, sink_mode: str = "exp",
+                                        num_splits=None, *, s_aux=None, sink_mode: str = "linear",
                                         sm_scale: float | None = None):
     """Dense-cache split-KV decode over tokens [start_k_offsets[b], cache_lens[b]).
 
@@ -231,7 +235,7 @@ def flash_decode_gqa_hf_fp8(q_fp8, k_cache_fp8, v_cache_fp8, cache_lens, scale_q
 # ---------------------------------------------------------------------------
 def paged_flash_decode(q, k_pool, v_pool, block_table, seq_lens, page_size, *, s_aux=None,
                        k_scale=None, v_scale=None, out_dtype: torch.dtype | None = None,
-                       sink_mode: str = "exp", sm_scale: float | None = None,
+                       sink_mode: str = "linear", sm_scale: float | None = None,
                        chunk_tokens: int = 0, return_block_scores: bool = False,
                        score_blocks: int | None = None):
     """Paged GQA decode through a block table.

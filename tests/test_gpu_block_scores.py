@@ -1,8 +1,9 @@
 """GPU parity of the pooled block scores (the TileLang kernel's S output)
 against the float64 oracle: varlen and paged, f16 / bf16 / e4m3 KV, both sink
 modes, lengths around block boundaries and zero, truncated and padded score
-widths, fixed and automatic split sizes.  Bar: atol = rtol = 2e-3 plus half
-an ulp of the score dtype; blocks past a sequence are exactly 0.
+widths, fixed and automatic split sizes.  Bar: atol = rtol = 2e-3 (plus half
+an ulp for bf16 scores, the final cast's own rounding); blocks past a
+sequence are exactly 0.
 """
 import numpy as np
 import pytest
@@ -18,7 +19,7 @@ DEV = "cuda"
 
 def close(got, want, what):
     g = got.double().cpu().numpy()
-    half_ulp = np.abs(want) * {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8, torch.float32: 0.0}[got.dtype]
+    half_ulp = np.abs(want) * (2.0 ** -8 if got.dtype == torch.bfloat16 else 0.0)  # bf16 scores only
     tol = 2e-3 + 2e-3 * np.abs(want) + half_ulp
     bad = ~(np.abs(g - want) <= tol)
     assert not bad.any(), f"{what}: {bad.sum()} bad, first {np.argwhere(bad)[0]}, got {g[bad][:3]}, want {want[bad][:3]}"
@@ -69,7 +70,8 @@ def test_paged_block_scores(kv):
     wl = W.make(name, overrides=dict(B=6, lens=("list", [5, 128, 300, 2000, 4097, 0])), seed=7)
     d = wl.to(DEV)
     out, S = paged_flash_decode(d.q, d.k, d.v, d.block_table, d.seq_lens, 16, s_aux=d.s_aux, k_scale=d.k_scale,
-                                v_scale=d.v_scale, out_dtype=d.out_dtype, return_block_scores=True)
+                                v_scale=d.v_scale, out_dtype=d.out_dtype, sink_mode="exp",
+                                return_block_scores=True)
     torch.cuda.synchronize()
     assert S.shape == (6, 32, -(-wl.block_table.shape[1] * 16 // 128))
     if kv == "e4m3":
@@ -132,14 +134,15 @@ def test_block_scores_bench_sizes(name):
     d = wl.to(DEV)
     if wl.layout == "paged":
         out, S = paged_flash_decode(d.q, d.k, d.v, d.block_table, d.seq_lens, 16, s_aux=d.s_aux,
-                                    return_block_scores=True)
+                                    sink_mode="exp", return_block_scores=True)
         want = O.block_scores_paged(wl.q.double().numpy(), wl.k.numpy(), wl.block_table.numpy(), wl.lens,
                                     None if wl.s_aux is None else wl.s_aux.double().numpy(), "exp",
                                     n_blocks=S.shape[2])
         ref = O.decode_paged(wl.q.double().numpy(), wl.k.numpy(), wl.v.numpy(), wl.block_table.numpy(), wl.lens,
                              None if wl.s_aux is None else wl.s_aux.double().numpy())
     else:
-        out, S = flash_decode_gqa_varlen(d.q, d.k, d.v, d.cu_seqlens, d.s_aux, return_block_scores=True)
+        out, S = flash_decode_gqa_varlen(d.q, d.k, d.v, d.cu_seqlens, d.s_aux, sink_mode="exp",
+                                         return_block_scores=True)
         want = O.block_scores_varlen(wl.q.double().numpy(), wl.k.numpy(), wl.cu_seqlens.numpy(),
                                      wl.s_aux.double().numpy(), "exp", n_blocks=S.shape[2])
         ref = O.decode_varlen(wl.q.double().numpy(), wl.k.double().numpy(), wl.v.double().numpy(),

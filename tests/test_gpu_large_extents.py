@@ -122,7 +122,7 @@ def test_varlen_rows_beyond_4gib():
     v.copy_(vc.to(DEV))
     for chunk in (0, 32):
         out = dec.flash_decode_gqa_varlen(q.to(DEV), k, v, torch.tensor(cu, dtype=torch.int32, device=DEV),
-                                          s_aux.to(DEV), chunk_tokens=chunk)
+                                          s_aux.to(DEV), sink_mode="exp", chunk_tokens=chunk)
         torch.cuda.synchronize()
         assert_close(out, ref, 2e-3, 2e-3, f"varlen rows beyond 4 GiB, chunk_tokens={chunk}")
     del buf, k, v, out
