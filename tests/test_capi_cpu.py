@@ -398,3 +398,38 @@ def test_workspace_bytes_with_a_chunk_cap(lib):
         for cap in (-32, -96, -512, -4096, -8192):
             assert lib.fsk_workspace_bytes(layout, 4, 32, 8, 128, extent, 16, cap) >= auto > 0, (layout, cap)
         assert lib.fsk_workspace_bytes(layout, 4, 32, 8, 128, extent, 16, -48) == nat.FSK_ERR_INVALID
+
+
+def header_param_count(name):
+    """Number of parameters of ``name``'s prototype in the header."""
+    text = open(HEADER).read()
+    m = re.search(r"FSK_API\s+[\w\s\*]+?\b" + name + r"\s*\((.*?)\);", text, flags=re.S)
+    assert m, name
+    return len([p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"])
+
+
+def test_reference_side_binding_signature(lib):
+    """The ctypes-only binding a reference maintainer would add
+    (fasterkernels_amd/reference_binding.py) declares fsk_decode_varlen and
+    fsk_workspace_bytes exactly as the package's own binding and the header
+    do, and loads the library without a GPU."""
+    from fasterkernels_amd import reference_binding as rb
+    assert rb.VARLEN_ARGTYPES == nat.SIGNATURES["fsk_decode_varlen"][1]
+    assert len(rb.VARLEN_ARGTYPES) == header_param_count("fsk_decode_varlen")
+    assert rb.WORKSPACE_ARGTYPES == nat.SIGNATURES["fsk_workspace_bytes"][1]
+    assert len(rb.WORKSPACE_ARGTYPES) == header_param_count("fsk_workspace_bytes")
+    assert rb.FSK_SINK_LINEAR == nat.FSK_SINK_LINEAR and rb.FSK_LAYOUT_VARLEN == nat.FSK_LAYOUT_VARLEN
+    rlib = rb.load(nat.LIB_PATH)
+    assert rlib.fsk_decode_varlen.argtypes == rb.VARLEN_ARGTYPES
+    assert rlib.fsk_workspace_bytes(0, 4, 32, 8, 128, 4096, 16, 0) == lib.fsk_workspace_bytes(0, 4, 32, 8, 128, 4096,
+                                                                                            16, 0) > 0
+    q = torch.zeros(2, 32, 128, dtype=torch.float16)
+    k = torch.zeros(4, 8, 128, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="must be a CUDA"):
+        rb.flash_decode_gqa_varlen(q, k, k, torch.tensor([0, 1, 2], dtype=torch.int32))
+
+
+def test_every_signature_matches_the_header_arity():
+    """Each ctypes signature has as many parameters as its prototype."""
+    for name, (_, args) in nat.SIGNATURES.items():
+        assert len(args) == header_param_count(name), name
