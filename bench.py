@@ -26,6 +26,17 @@ dtypes over the same workload, median of >= 3 runs, with the thread count.  The 
 warm-up (300 steps) covers the ~20 ms the shader clock takes to settle under
 load.
 
+The default run (M0 with no other workload options) then times the other
+decode configurations, C1..C5, the same way and adds them under ``configs``:
+each with its own warm-up and step count set from elapsed time (about 0.3 s
+of each, stated in the entry), its partial kernel's roofline (with the
+counter traffic of profiles/partial_kernel_<config>_traffic.md) and a CPU
+baseline of about 3 s.  ``--configs C2,C4`` picks others, ``--configs ''``
+none.  ``--sweep`` runs only the reference benchmark's own sweep
+(benchmarks/benchmark.py:20-33, 150-158: varlen fp16, lengths uniform in
+[max(64, S/4), S], sinks 0.1 N(0,1) folded linearly; S = 512..32768 at B=4
+and B = 1..32 at S=16384), one JSON line per point.
+
 Other workloads: ``--config C1..C5`` (decode configurations), ``--config M0b``
 (M0 with bf16 Q, KV and output), ``--config G1`` (varlen with sinks at head_dim
 64, Hq=64, Hkv=8), ``--config G2`` (paged at head_dim 256, 16384 tokens per
@@ -38,6 +49,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -78,6 +90,12 @@ def parse():
     ap.add_argument("--wave-stamps", action="store_true",
                     help="load the wave-stamp build and print the partial kernel's per-wave timeline "
                          "(start-up, streaming, tail, dispatch) instead of the benchmark line")
+    ap.add_argument("--configs", default=None, metavar="C1,C2,...",
+                    help="decode configurations timed after the headline, each with a time-based warm-up and "
+                         "step count (default with a plain M0 run: C1..C5; '' for none)")
+    ap.add_argument("--sweep", action="store_true",
+                    help="only the reference benchmark's sweep (varlen fp16, lengths U[max(64,S/4), S], "
+                         "sinks 0.1 N(0,1), linear fold): S = 512..32768 at B=4, B = 1..32 at S=16384")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration under rocprof)")
     return ap.parse_args()
@@ -462,6 +480,206 @@ def wave_timeline(args):
                       "options": args.option, "algorithmic_bytes": base.algorithmic_bytes(), **med}), flush=True)
 
 
+# Decode configurations timed beside the headline in the default run (the
+# other decode configurations of the benchmark definition).  Each gets its own
+# warm-up and step count, set from elapsed time (the headline keeps the counts
+# the command line gives), and a bounded CPU-baseline budget.
+SUB_CONFIGS = ("C1", "C2", "C3", "C4", "C5")
+SUB_WARMUP_S = 0.3    # warm-up: at least this long (and at least 50 steps in all)
+SUB_TIMED_S = 0.3     # timed steps: about this long (100 to 5000 steps)
+SUB_CPU_S = 3.0       # CPU-baseline budget per configuration (seconds)
+
+
+def decode_sets(config: str, dev, layers: int = 1, sets: int = 0):
+    """The rotating input sets of a decode workload: the same lengths and page
+    tables with independent Q/K/V data, at least 4 sets and a footprint above
+    1.1 GB, in whole groups of ``layers``."""
+    from fasterkernels_amd import workloads as W
+    base = W.make(config, gen_device=dev, device=dev)
+    kv_bytes = base.k.numel() * base.k.element_size() * 2
+    n_sets = sets or rotation_sets(kv_bytes)
+    n_sets = -(-max(n_sets, layers) // layers) * layers
+    out = [base] + [W.make(config, gen_device=dev, device=dev, data_seed=base.meta["seed"] + 1000 * i)
+                    for i in range(1, n_sets)]
+    assert all(s.lens == base.lens for s in out)
+    return out
+
+
+def timed_pass(step, steps: int, warmup: int):
+    """``warmup`` untimed steps, then ``steps`` timed ones between two
+    synchronisations, then the median pass.  Returns (elapsed s, host issue
+    s, median µs per step)."""
+    import torch
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i)
+    issued = time.perf_counter() - t0   # host time to issue the steps (the host-bound limit)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    return elapsed, issued, median_step_us(step, steps, steps)
+
+
+def time_based_counts(step, warm_s: float, timed_s: float):
+    """(warm-up steps, timed steps) for a configuration: a step time estimated
+    from 10 steps after 10 others (those 20 count towards the warm-up), then
+    a warm-up of at least ``warm_s`` and a timed region of about ``timed_s``."""
+    import torch
+    for i in range(10):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(10, 20):
+        step(i)
+    torch.cuda.synchronize()
+    est = max((time.perf_counter() - t0) / 10, 1e-6)
+    warmup = max(30, int(math.ceil(warm_s / est)))
+    steps = min(5000, max(100, int(math.ceil(timed_s / est))))
+    return 20 + warmup, steps, est
+
+
+def decode_kernel_pass(sets, n_steps: int, chunk: int, block_scores: bool, layers: int):
+    """A further pass of ``n_steps`` steps with every decode call's partial
+    and reduce kernels stamped by their own dispatches.  Returns (partial ms,
+    partial-start-to-reduce-end ms, calls) summed."""
+    from fasterkernels_amd import native as nat
+    from fasterkernels_amd import workloads as W
+    n_sets = len(sets)
+    nat.enable_kernel_timing(KT_EVERY)
+    for i in range(n_steps):
+        for j in range(layers):
+            W.run(sets[(i * layers + j) % n_sets], chunk_tokens=chunk, block_scores=block_scores)
+    part_ms, tot_ms, calls = nat.kernel_timing()
+    nat.enable_kernel_timing(0)
+    return part_ms, tot_ms, calls
+
+
+def traffic_path(config: str, kernel: str = "partial_kernel") -> str:
+    return os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"{kernel}_{config}_traffic.md")
+
+
+def dtype_name(t) -> str:
+    import torch
+    return {torch.float16: "f16", torch.bfloat16: "bf16", torch.float8_e4m3fn: "e4m3"}[t]
+
+
+def workload_name(config: str, wl) -> str:
+    return (f"{config}: {wl.layout} GQA decode B={wl.B} Hq={wl.Hq} Hkv={wl.Hkv} D={wl.D} "
+            f"tokens={wl.total_tokens} kv={str(wl.k.dtype).replace('torch.', '')}")
+
+
+def measure_decode(sets, *, sink_mode: str = "exp", warm_s: float = SUB_WARMUP_S,
+                   timed_s: float = SUB_TIMED_S) -> dict:
+    """Step and kernel timing of eager decode calls over rotating input sets,
+    with a time-based warm-up and step count (see time_based_counts)."""
+    from fasterkernels_amd import native as nat
+    from fasterkernels_amd import workloads as W
+    n_sets = len(sets)
+
+    def step(i):
+        return W.run(sets[i % n_sets], sink_mode=sink_mode)
+
+    warmup, steps, est = time_based_counts(step, warm_s, timed_s)
+    elapsed, issued, med_us = timed_pass(step, steps, warmup - 20)
+    nat.enable_kernel_timing(KT_EVERY)
+    for i in range(kernel_timing_steps(steps)):
+        step(steps + i)
+    part_ms, tot_ms, calls = nat.kernel_timing()
+    nat.enable_kernel_timing(0)
+    base = sets[0]
+    alg = base.algorithmic_bytes()
+    us_step = elapsed * 1e6 / steps
+    part_us = part_ms * 1e3 / max(calls, 1)
+    kern_gbs = alg / (part_us * 1e-6) / 1e9 if part_us > 0 else None
+    gbs = alg / (us_step * 1e-6) / 1e9
+    return {
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "us_per_step": round(us_step, 2),
+        "us_per_step_median": round(med_us, 2),
+        "host_us_per_step": round(issued * 1e6 / steps, 2),
+        "ms_per_step": round(us_step / 1e3, 5),
+        "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+        "steps": steps,
+        "warmup": warmup,
+        "warmup_rule": f"{warm_s} s of steps (>= 30) after a 20-step estimate; timed steps ~{timed_s} s "
+                       f"(100..5000); estimate {est * 1e6:.1f} us/step",
+        "dtype": dtype_name(base.k.dtype),
+        "data": f"synthetic N(0,1), generated on device, {n_sets} rotating input sets",
+        "batch": base.B, "total_tokens": base.total_tokens, "algorithmic_bytes": alg,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": None if kern_gbs is None else round(kern_gbs, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": None if kern_gbs is None else round(kern_gbs / PEAK_HBM_GBS, 4),
+            "kernel": "partial_kernel (split-KV partials)",
+            "kernel_avg_us": round(part_us, 3),
+            "partial_plus_reduce_avg_us": round(tot_ms * 1e3 / max(calls, 1), 3),
+            "kernel_calls_timed": calls,
+        },
+    }
+
+
+def release(sets) -> None:
+    import torch
+    sets.clear()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def sub_config(config: str, dev, cpu_seconds: float, no_cpu: bool) -> dict:
+    """One decode configuration measured the way the headline is (rotating
+    HBM-resident inputs, eager decode calls, the partial kernel timed by its
+    own dispatches), with a time-based warm-up and step count."""
+    t_start = time.perf_counter()
+    sets = decode_sets(config, dev)
+    m = measure_decode(sets)
+    entry = {"workload": workload_name(config, sets[0]),
+             "sinks": None if sets[0].s_aux is None else "N(0,1), exp fold (sink logit)", **m}
+    entry["roofline"]["traffic"] = read_traffic(traffic_path(config))
+    entry["cpu_baseline"] = None if no_cpu else cpu_baseline(sets[0], cpu_seconds)
+    release(sets)
+    entry["wall_s"] = round(time.perf_counter() - t_start, 2)
+    return entry
+
+
+# The reference's own benchmark sweep (benchmarks/benchmark.py:150-158):
+# maximum length at B=4, then batch at a maximum length of 16384.
+SWEEP_SEQ_LENS = (512, 1024, 2048, 4096, 8192, 16384, 32768)
+SWEEP_BATCHES = (1, 2, 4, 8, 16, 32)
+
+
+def reference_sweep(args) -> None:
+    """The reference benchmark's workload on this GPU: varlen fp16 decode,
+    Hq=32, Hkv=8, D=128, lengths uniform in [max(64, S/4), S], sinks
+    0.1 N(0,1) folded linearly (as the reference kernels do); one JSON line
+    per point, then a summary line."""
+    import torch
+
+    from fasterkernels_amd import workloads as W
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    points = [("seq_len", 4, S) for S in SWEEP_SEQ_LENS] + [("batch", B, 16384) for B in SWEEP_BATCHES]
+    rows = []
+    for kind, B, S in points:
+        base = W.reference_sweep_workload(B, S, gen_device=dev, device=dev)
+        n_sets = rotation_sets(base.k.numel() * base.k.element_size() * 2)
+        sets = [base] + [W.reference_sweep_workload(B, S, gen_device=dev, device=dev, data_seed=4200 + i)
+                         for i in range(1, n_sets)]
+        m = measure_decode(sets, sink_mode="linear")
+        row = {"sweep": kind, "B": B, "max_S": S, "lens": list(base.lens), **m}
+        release(sets)
+        rows.append(row)
+        print(json.dumps(row), flush=True)
+    print(json.dumps({"reference_sweep": [{k: r[k] for k in ("sweep", "B", "max_S", "total_tokens",
+                                                          "us_per_step", "us_per_step_median", "value")}
+                                           | {"kernel_us": r["roofline"]["kernel_avg_us"],
+                                              "frac": r["roofline"]["frac"]} for r in rows]}), flush=True)
+
+
 def main():
     args = parse()
     if args.wave_stamps:
@@ -485,21 +703,19 @@ def main():
     if args.config in W.WRITE_CONFIGS:
         bench_write(args)
         return
+    if args.sweep:
+        reference_sweep(args)
+        return
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     nat.set_option("qk_engine", 1 if args.qk_engine == "valu" else 0)
     for opt in args.option:
         name, _, value = opt.partition("=")
         nat.set_option(name, int(value))
-    base = W.make(args.config, gen_device=dev, device=dev)
-    kv_bytes = base.k.numel() * base.k.element_size() * 2
     L = max(1, args.layers)
-    n_sets = args.sets or rotation_sets(kv_bytes)
-    n_sets = -(-max(n_sets, L) // L) * L     # whole groups of L layers
-    # same lengths and page tables, independent K/V data
-    sets = [base] + [W.make(args.config, gen_device=dev, device=dev, data_seed=base.meta["seed"] + 1000 * i)
-                     for i in range(1, n_sets)]
-    assert all(s.lens == base.lens for s in sets)
+    sets = decode_sets(args.config, dev, L, args.sets)
+    base = sets[0]
+    n_sets = len(sets)
     alg_bytes = base.algorithmic_bytes() * L
     writes = [W.step_write(s, seed=5000 + i) for i, s in enumerate(sets)] if args.with_write else None
     if args.with_write:
@@ -525,16 +741,7 @@ def main():
         def step(i):
             return layer_calls(i % n_groups)
 
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    issued = time.perf_counter() - t0   # host time to issue the steps (the host-bound limit)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    med_us = median_step_us(step, args.steps, args.steps)
+    elapsed, issued, med_us = timed_pass(step, args.steps, args.warmup)
     # Kernel durations: a second timed pass of the same steps, with timing on
     # the calls KT_EVERY selects (the timing costs host time, so it stays out
     # of the step timing above).
@@ -558,12 +765,7 @@ def main():
     else:
         # the partial and reduce kernels stamped by their own dispatches
         # (decode calls only: the write kernels' stamps would join the triples)
-        nat.enable_kernel_timing(KT_EVERY)
-        for i in range(n_kt):
-            for j in range(L):
-                W.run(sets[(i * L + j) % n_sets], chunk_tokens=args.chunk, block_scores=args.block_scores)
-        part_ms, tot_ms, calls = nat.kernel_timing()
-        nat.enable_kernel_timing(0)
+        part_ms, tot_ms, calls = decode_kernel_pass(sets, n_kt, args.chunk, args.block_scores, L)
 
     ms_step = elapsed * 1e3 / args.steps
     gbs = alg_bytes / (ms_step / 1e3) / 1e9
@@ -572,10 +774,8 @@ def main():
         part_avg_ms = tot_ms / max(calls, 1)
     call_bytes = base.algorithmic_bytes()
     kern_gbs = call_bytes / (part_avg_ms / 1e3) / 1e9 if part_avg_ms > 0 else None
-    traffic_file = args.traffic or os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                                                f"partial_kernel_{args.config}_traffic.md")
-    traffic = (None if (args.chunk or args.graph or args.block_scores or args.qk_engine != "mfma" or args.option
-                        or L > 1) else read_traffic(traffic_file))
+    plain = not (args.chunk or args.graph or args.block_scores or args.qk_engine != "mfma" or args.option or L > 1)
+    traffic = read_traffic(args.traffic or traffic_path(args.config)) if plain else None
 
     out = {
         "metric": METRIC if (args.config == "M0" and L == 1) else (
@@ -594,11 +794,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {torch.float16: "f16", torch.bfloat16: "bf16", torch.float8_e4m3fn: "e4m3"}[base.k.dtype],
+        "dtype": dtype_name(base.k.dtype),
         "data": f"synthetic N(0,1), generated on device, {n_sets} rotating input sets",
         "config": {
-            "workload": f"{args.config}: {base.layout} GQA decode B={base.B} Hq={base.Hq} Hkv={base.Hkv} "
-                        f"D={base.D} tokens={base.total_tokens} kv={str(base.k.dtype).replace('torch.', '')}",
+            "workload": workload_name(args.config, base),
             "batch": base.B, "total_tokens": base.total_tokens, "algorithmic_bytes": alg_bytes,
             "chunk_tokens": args.chunk or "auto",
             "launch": "hip graph replay" if args.graph else "eager",
@@ -625,6 +824,21 @@ def main():
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(sets[0], args.cpu_seconds)
+    del sets, base, writes
+    if args.graph:
+        del graphs
+    subs = [c.strip() for c in args.configs.split(",") if c.strip()] if args.configs else []
+    if args.configs is None and args.config == "M0" and plain:
+        subs = list(SUB_CONFIGS)
+    if subs:
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        out["configs"] = {}
+        for name in subs:
+            if name not in W.CONFIGS:
+                raise SystemExit(f"--configs: unknown decode configuration {name!r}")
+            print(f"# timing {name}", file=sys.stderr, flush=True)
+            out["configs"][name] = sub_config(name, dev, SUB_CPU_S, args.no_cpu)
     print(json.dumps(out), flush=True)
 
 

@@ -194,8 +194,20 @@ def make(name: str = "M0", *, device=None, seed: int | None = None, overrides: d
         k, v = kf.to(kvdt), vf.to(kvdt)
     del kf, vf
     s_aux = _randn((Hq,), gd, rd).to(torch.float32) if cfg["sinks"] else None
+    if s_aux is not None and cfg.get("sink_scale", 1.0) != 1.0:
+        s_aux = s_aux * float(cfg["sink_scale"])
     wl = Workload(name, layout, B, Hq, Hkv, D, lens, q, k, v, cu, bt, sl, s_aux, ks, vs, odt, wl_meta)
     return wl.to(device) if device is not None else wl
+
+
+def reference_sweep_workload(B: int, S: int, *, device=None, gen_device=None, data_seed: int | None = None) -> Workload:
+    """The reference benchmark's decode input at batch B and maximum length S
+    (benchmarks/benchmark.py:20-33): varlen fp16, Hq=32, Hkv=8, D=128,
+    lengths uniform in [max(64, S // 4), S] (seed 42, drawn here from a CPU
+    generator), Q/K/V N(0,1), sinks 0.1 N(0,1), which the reference kernels
+    fold linearly."""
+    return make("C1", device=device, gen_device=gen_device, data_seed=data_seed, seed=42,
+                overrides=dict(B=B, lens=("uniform", max(64, S // 4), S), sinks=True, sink_scale=0.1))
 
 
 def run(wl: Workload, *, sink_mode: str = "exp", chunk_tokens: int = 0, block_scores: bool = False):
