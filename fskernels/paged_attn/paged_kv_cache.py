@@ -12,11 +12,17 @@ sequence reaches a page boundary.
 
 Page bookkeeping stays on the host, as in the reference, with a host mirror of
 every sequence's page list, so no call reads the device block table back (the
-reference does, with ``.item()``, at :96 and :126).  The rows themselves are
+reference does, with ``.item()``, at :96 and :126).  On a GPU the rows are
 stored by the gfx950 write kernel: one launch per call stores every token of a
-batch and the new block-table entries together, so the pools must live on a
-HIP device.  e4m3 pools (``dtype=torch.float8_e4m3fn``) can carry per-tensor
-``k_scale``/``v_scale``; rows are then quantised on the way in.
+batch and the new block-table entries together.  Like the reference's, the
+cache can also be built in host memory (``device="cpu"``, e.g. for a cache
+kept off the GPU); its rows are then stored with the reference's indexed
+assignment (:128-130) on the host.  That is where the pools live, chosen at
+construction, not a substitute for the kernel: GPU pools are only ever
+written by the kernel, and the decode entry points reject host pools.  e4m3
+pools (``dtype=torch.float8_e4m3fn``) can carry per-tensor
+``k_scale``/``v_scale``; rows are then quantised on the way in
+(``e4m3(clamp(x / scale, -448, 448))``, the same codes on both devices).
 """
 from __future__ import annotations
 
@@ -76,6 +82,7 @@ class PagedKVCache:
         self._active: List[bool] = [False] * self.max_seqs
         self._free_pages: List[int] = list(range(self.num_pages))
         self._pages: List[List[int]] = [[] for _ in range(self.max_seqs)]
+        self._journal = None  # (pages popped, {seq: (old length, old page count)}) of the call in progress
         if (self.k_scale is None) != (self.v_scale is None):
             raise ValueError("give both k_scale and v_scale or neither")
         if self.k_scale is not None:
@@ -121,7 +128,10 @@ class PagedKVCache:
     def _alloc_page(self) -> int:
         if not self._free_pages:
             raise RuntimeError("Out of KV pages")
-        return self._free_pages.pop()
+        pp = self._free_pages.pop()
+        if self._journal is not None:
+            self._journal[0].append(pp)
+        return pp
 
     # ------------------------------------------------------------------
     def _plan(self, seq_ids: Sequence[int], num_tokens: int = 1) -> Tuple[List[int], List[Tuple[int, int]]]:
@@ -146,9 +156,12 @@ class PagedKVCache:
         row_stride = self.block_table.stride(0)
         slots: List[int] = []
         updates: List[Tuple[int, int]] = []
+        touched = self._journal[1] if self._journal is not None else None
         for sid in seq_ids:
             pages = self._pages[sid]
             pos = self._seq_lens[sid]
+            if touched is not None and sid not in touched:
+                touched[sid] = (pos, len(pages))
             for _ in range(num_tokens):
                 lp, off = divmod(pos, PAGE_SIZE)
                 if off == 0:
@@ -164,8 +177,8 @@ class PagedKVCache:
 
     def _require_gpu(self):
         if not self.k_pool.is_cuda:
-            raise RuntimeError("PagedKVCache stores rows with the HIP write kernel; "
-                               f"its pools are on {self.k_pool.device}, not a GPU")
+            raise RuntimeError("this needs the cache's pools on a GPU (HIP) device; "
+                               f"they are on {self.k_pool.device}, not a GPU")
 
     def _new_rows(self, t, name: str, n: int) -> torch.Tensor:
         """New K or V rows for ``n`` tokens, checked before any bookkeeping
@@ -194,33 +207,64 @@ class PagedKVCache:
         """Restores the host bookkeeping (lengths, page lists, free list) if
         the body raises: planning, staging and the launch succeed together or
         leave no trace.  (The block-table stores ride the write launch, so a
-        call that fails before or at the launch has stored none.)"""
-        lens = list(self._seq_lens)
-        npages = [len(p) for p in self._pages]
-        free = list(self._free_pages)
+        call that fails before or at the launch has stored none.)  _plan
+        journals what it changes (the pages it pops, in order, and each
+        touched sequence's old length and page count), so the cost is that of
+        the call's own tokens, not of the pool or the batch."""
+        journal = ([], {})
+        self._journal = journal
         try:
             yield
         except BaseException:
-            self._seq_lens[:] = lens
-            for pages, n in zip(self._pages, npages):
-                del pages[n:]
-            self._free_pages[:] = free
+            popped, touched = journal
+            for sid, (length, n_pages) in touched.items():
+                self._seq_lens[sid] = length
+                del self._pages[sid][n_pages:]
+            self._free_pages.extend(reversed(popped))
             raise
+        finally:
+            self._journal = None
 
     def _stage(self, slots, updates):
-        """One host->device copy of the slots and block-table stores."""
+        """The slots and block-table stores as one int64 tensor on the pools'
+        device (one host->device copy for GPU pools)."""
         vals = list(slots)
         for flat, page in updates:
             vals += (flat, page)
-        host = torch.tensor(vals, dtype=torch.int64, pin_memory=True)
-        dev = host.to(self.k_pool.device, non_blocking=True)
+        if self.k_pool.is_cuda:
+            host = torch.tensor(vals, dtype=torch.int64, pin_memory=True)
+            dev = host.to(self.k_pool.device, non_blocking=True)
+        else:
+            dev = torch.tensor(vals, dtype=torch.int64)
         n = len(slots)
         return dev[:n], dev[n:].view(-1, 2)
 
     def _write(self, layer_idx, k, v, slot_dev, upd_dev):
-        paged_kv_write(k, v, self.k_pool[layer_idx], self.v_pool[layer_idx], slot_dev,
-                       k_scale=self.k_scale, v_scale=self.v_scale,
-                       block_table=self.block_table, bt_updates=upd_dev)
+        if self.k_pool.is_cuda:
+            paged_kv_write(k, v, self.k_pool[layer_idx], self.v_pool[layer_idx], slot_dev,
+                           k_scale=self.k_scale, v_scale=self.v_scale,
+                           block_table=self.block_table, bt_updates=upd_dev)
+        else:
+            self._write_host(layer_idx, k, v, slot_dev, upd_dev)
+
+    def _write_host(self, layer_idx, k, v, slots, upd=None):
+        """Host-memory pools: the reference's block-table store and indexed
+        row stores (paged_kv_cache.py:122-130) for every token at once, with
+        the write kernel's rules (slots outside the pool are skipped; e4m3
+        pools with scales store e4m3(clamp(x / scale, -448, 448)))."""
+        if upd is not None and upd.numel():
+            self.block_table.view(-1)[upd[:, 0]] = upd[:, 1].to(torch.int32)
+        n = slots.numel()
+        if n == 0:
+            return
+        slots = slots.reshape(n).to(torch.int64)
+        ok = (slots >= 0) & (slots < self.num_pages * PAGE_SIZE)
+        pages, rows = slots[ok] // PAGE_SIZE, slots[ok] % PAGE_SIZE
+        for pool, x, scale in ((self.k_pool[layer_idx], k, self.k_scale), (self.v_pool[layer_idx], v, self.v_scale)):
+            x = x.reshape(n, self.num_kv_heads, self.head_dim)[ok]
+            if scale is not None:
+                x = (x.to(torch.float32) / scale).clamp(-448.0, 448.0)
+            pool[pages, :, rows, :] = x.to(pool.dtype)
 
     # ------------------------------------------------------------------
     def append_kv(self, seq_id: int, layer_idx: int, k: torch.Tensor, v: torch.Tensor):
@@ -236,7 +280,6 @@ class PagedKVCache:
         """append_kv for several tokens in one launch: token j of k/v
         ([n, Hkv, 1, D] or [n, Hkv, D]) goes to sequence seq_ids[j]; the
         bookkeeping is that of n append_kv calls in order."""
-        self._require_gpu()
         n = len(seq_ids)
         k = self._new_rows(k, "k", n)
         v = self._new_rows(v, "v", n)
@@ -251,8 +294,7 @@ class PagedKVCache:
         """Takes ``num_tokens`` new positions in each listed sequence (pages as
         needed, block table stored on the device) and returns their slots, an
         int64 device tensor [len(seq_ids) * num_tokens], sequence-major, for
-        ``write_kv`` of every layer."""
-        self._require_gpu()
+        ``write_kv`` of every layer (a host tensor for host pools)."""
         with self._all_or_nothing():
             slots, updates = self._plan(list(seq_ids), int(num_tokens))
             slot_dev, upd_dev = self._stage(slots, updates)
@@ -264,9 +306,14 @@ class PagedKVCache:
     def write_kv(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor):
         """Stores rows k/v ([n, Hkv, D], any strides with a contiguous head_dim,
         or [n, Hkv, 1, D]) of one layer at slots from ``reserve_slots``."""
-        self._require_gpu()
-        paged_kv_write(k, v, self.k_pool[layer_idx], self.v_pool[layer_idx], slot_mapping,
-                       k_scale=self.k_scale, v_scale=self.v_scale)
+        if self.k_pool.is_cuda:
+            paged_kv_write(k, v, self.k_pool[layer_idx], self.v_pool[layer_idx], slot_mapping,
+                           k_scale=self.k_scale, v_scale=self.v_scale)
+        else:
+            n = slot_mapping.numel()
+            k = self._new_rows(k, "k", n)
+            v = self._new_rows(v, "v", n)
+            self._write_host(layer_idx, k, v, slot_mapping.to(self.k_pool.device))
 
     # ------------------------------------------------------------------
     def get_block_table_tensor(self, active_seq_ids: List[int]) -> torch.Tensor:

@@ -222,9 +222,10 @@ def fits(ref, ids, n_tok, max_blocks):
     return need <= len(ref.free_pages) and max(-(-a // 16) for a in after.values()) <= max_blocks
 
 
-def run_cache_script(cache, ref, rnd, steps, layers, src_dt, gen):
+def run_cache_script(cache, ref, rnd, steps, layers, src_dt, gen, dev=DEV):
     """Random allocate / append / batch-append / reserve+write / free steps on
-    both caches, comparing the full state after every step."""
+    both caches, comparing the full state after every step (the cache's
+    pools and new rows on ``dev``)."""
     live = []
     hkv, d = cache.num_kv_heads, cache.head_dim
     mb = cache.max_blocks_per_seq
@@ -246,14 +247,14 @@ def run_cache_script(cache, ref, rnd, steps, layers, src_dt, gen):
             if not fits(ref, [sid], 1, mb):
                 continue
             x = torch.randn(2, 1, hkv, 1, d, generator=gen).to(src_dt)
-            cache.append_kv(sid, layer, x[0].to(DEV), x[1].to(DEV))
+            cache.append_kv(sid, layer, x[0].to(dev), x[1].to(dev))
             ref.append_kv(sid, layer, x[0, 0, :, 0].float().numpy(), x[1, 0, :, 0].float().numpy())
         elif op < 0.75:     # one token for several sequences in one launch
             ids = [rnd.choice(live) for _ in range(rnd.randint(1, 5))]
             if not fits(ref, ids, 1, mb):
                 continue
             x = torch.randn(2, len(ids), hkv, 1, d, generator=gen).to(src_dt)
-            cache.append_kv_batch(ids, layer, x[0].to(DEV), x[1].to(DEV))
+            cache.append_kv_batch(ids, layer, x[0].to(dev), x[1].to(dev))
             for j, sid in enumerate(ids):
                 ref.append_kv(sid, layer, x[0, j, :, 0].float().numpy(), x[1, j, :, 0].float().numpy())
         else:               # reserve a span once, store it for every layer
@@ -264,7 +265,7 @@ def run_cache_script(cache, ref, rnd, steps, layers, src_dt, gen):
             slots = cache.reserve_slots(ids, n_tok)
             xs = [torch.randn(2, len(ids) * n_tok, hkv, d, generator=gen).to(src_dt) for _ in range(layers)]
             for lyr in range(layers):
-                cache.write_kv(lyr, xs[lyr][0].to(DEV), xs[lyr][1].to(DEV), slots)
+                cache.write_kv(lyr, xs[lyr][0].to(dev), xs[lyr][1].to(dev), slots)
             for j, sid in enumerate(ids):
                 for t in range(n_tok):
                     row = j * n_tok + t
@@ -273,7 +274,8 @@ def run_cache_script(cache, ref, rnd, steps, layers, src_dt, gen):
                     for lyr in range(1, layers):
                         ref_store(ref, sid, pos, lyr, xs[lyr][0, row].float().numpy(),
                                   xs[lyr][1, row].float().numpy())
-        torch.cuda.synchronize()
+        if torch.device(dev).type == "cuda":
+            torch.cuda.synchronize()
         assert cache.block_table.cpu().numpy().tolist() == ref.block_table.tolist(), step
         assert cache._seq_lens == ref.seq_lens and cache._free_pages == ref.free_pages, step
     return live
@@ -326,7 +328,7 @@ def test_decode_through_the_cache(pool):
     want = np.stack([O.attend(q[i].double().numpy(), *dense[i]) for i in range(len(lens))])
     atol = 1e-2 if scales else 2e-3
     err = np.abs(out.double().cpu().numpy() - want)
-    tol = atol + 2e-3 * np.abs(want) + np.abs(want) * 2.0 ** -11   # plus half an fp16 ulp
+    tol = atol + 2e-3 * np.abs(want)
     assert (err <= tol).all(), (err / tol).max()
 
 

@@ -1,7 +1,7 @@
 """PagedKVCache host logic on the CPU: page bookkeeping, block-table stores and
 slots, against the oracle's restatement of fskernels/paged_attn/paged_kv_cache.py
-(RefPagedKVCache).  Row stores need the HIP write kernel and are covered by the
-GPU tests; here they must refuse to run."""
+(RefPagedKVCache), and caches built in host memory, whose rows are stored on
+the host (GPU pools are written by the HIP write kernel: the GPU tests)."""
 import random
 import types
 
@@ -164,15 +164,66 @@ def test_planned_slots_decode_like_dense_attention():
     assert np.allclose(got, want, atol=1e-12)
 
 
-def test_row_stores_refuse_host_pools():
-    c = make()
+@pytest.mark.parametrize("pool,src", [("f16", "f16"), ("bf16", "bf16"), ("f16", "f32"), ("bf16", "f16"),
+                                      ("e4m3", "bf16"), ("e4m3", "f32")])
+def test_host_pools_match_reference_cache(pool, src):
+    """A cache built in host memory (device="cpu", which the reference's
+    cache allows) stores its rows on the host: driven by the same random
+    allocate / append / batch-append / reserve+write / free script as the GPU
+    test, it ends bit-identical to the oracle's restatement of the reference
+    cache (e4m3 pools with fixed scales quantise as the reference's
+    quantiser does)."""
+    import random
+    from tests.test_gpu_kv_write import POOL, SRC, compare, run_cache_script
+    rnd = random.Random(6)
+    gen = torch.Generator().manual_seed(6)
+    L, P, S, MB, hkv, d = 2, 64, 4, 16, 2, 32
+    scales = dict(k_scale=0.03, v_scale=0.02) if pool == "e4m3" else {}
+    cache = PagedKVCache(L, P, S, MB, hkv, d, POOL[pool], "cpu", **scales)
+    ref = O.RefPagedKVCache(L, P, S, MB, hkv, d, pool,
+                            np.float32(0.03) if scales else None, np.float32(0.02) if scales else None)
+    run_cache_script(cache, ref, rnd, 80, L, SRC[src], gen, dev="cpu")
+    compare(cache.k_pool, ref.k_pool, pool, src, "k_pool")
+    compare(cache.v_pool, ref.v_pool, pool, src, "v_pool")
+
+
+def test_host_pools_skip_out_of_range_slots_and_reject_decode():
+    """write_kv on host pools follows the write kernel's rule (a negative slot
+    or one past the pool is skipped), and the decode entry points refuse host
+    pools (no decode runs on the host)."""
+    from fskernels.paged_attn import paged_flash_decode
+    c = make(num_pages=2)
+    x = torch.arange(3 * 2 * 8, dtype=torch.float32).view(3, 2, 8)
+    c.write_kv(1, x, -x, torch.tensor([-1, 2 * 16, 17]))
+    assert torch.equal(c.k_pool[1, 1, :, 1], x[2].half()) and torch.equal(c.v_pool[1, 1, :, 1], -x[2].half())
+    c.k_pool[1, 1, :, 1] = 0
+    assert (c.k_pool == 0).all()
     s = c.allocate_sequence()
-    k = torch.zeros(1, 2, 1, 8, dtype=torch.float16)
-    with pytest.raises(RuntimeError, match="not a GPU"):
-        c.append_kv(s, 0, k, k)
-    with pytest.raises(RuntimeError, match="not a GPU"):
-        c.reserve_slots([s])
-    assert c._seq_lens[s] == 0 and c.pages_free == 8   # nothing was planned
+    c.append_kv(s, 0, torch.ones(1, 2, 1, 8), torch.ones(1, 2, 1, 8))
+    q = torch.zeros(1, 4, 8, dtype=torch.float16)
+    with pytest.raises(RuntimeError):
+        paged_flash_decode(q, c.k_pool[0], c.v_pool[0], c.get_block_table_tensor([s]), c.get_seq_lens_tensor([s]),
+                           PAGE_SIZE)
+
+
+def test_failed_call_restores_only_what_it_touched(monkeypatch):
+    """The rollback journal: a failed reservation puts back exactly the pages
+    it popped, in free-list order, and the lengths and page lists of the
+    sequences it touched, leaving the others alone."""
+    c = make(num_pages=8, max_seqs=3, max_blocks=4)
+    a, b, z = c.allocate_sequence(), c.allocate_sequence(), c.allocate_sequence()
+    c.reserve_slots([a], 20)     # pages 7, 6
+    c.reserve_slots([z], 3)      # page 5
+    before = _host_state(c)
+
+    def boom(*args, **kw):
+        raise RuntimeError("stage failed")
+    monkeypatch.setattr(c, "_stage", boom)
+    with pytest.raises(RuntimeError, match="stage failed"):
+        c.reserve_slots([b, a, b], 13)    # pops 4 (b), 3 (a: 20 -> 33), 2 (b: 13 -> 26)
+    after = _host_state(c)
+    assert after[:3] == before[:3] and torch.equal(after[3], before[3])
+    assert c._journal is None
 
 
 def _host_state(c):
