@@ -38,9 +38,10 @@
 
 // Device scratch of the allocation-free entry point fsk_decode_paged_noalloc:
 // the decode workspace (plan, partial maxima/sums, partial outputs) lives in
-// this file-scope array instead of caller- or library-allocated memory.  Every
-// device the library runs on holds its own copy (FSK_NOALLOC_SCRATCH_BYTES)
-// from the first call on that device until the process ends.  In host code
+// this file-scope array instead of caller- or library-allocated memory.  The
+// array belongs to the library's code object, so every device on which the
+// code object is loaded (any kernel of the library launched there) holds its
+// own copy of FSK_NOALLOC_SCRATCH_BYTES until the process ends.  In host code
 // the name is only a host-side stand-in: the device address comes from
 // hipGetSymbolAddress, once per device (see noalloc_scratch).
 static __device__ __align__(256) uint8_t scratch[FSK_NOALLOC_SCRATCH_BYTES];
@@ -1563,6 +1564,12 @@ constexpr int kWriteThreads = 256;
 #ifndef FSK_WRITE_NT
 #define FSK_WRITE_NT 1
 #endif
+// 1: a thread issues its source-row load together with the slot load (the
+// row's address does not depend on the slot; a skipped token's row is read
+// and dropped), so a step costs one memory round trip instead of two.
+#ifndef FSK_WRITE_EARLY
+#define FSK_WRITE_EARLY 0
+#endif
 constexpr int kWriteUnroll = FSK_WRITE_UNROLL;
 
 template <typename T>
@@ -1688,10 +1695,11 @@ __global__ __launch_bounds__(kWriteThreads) void kv_write_kernel(WriteParams p) 
       const uint32_t i = fdiv(row, p.hkv);
       const uint32_t h = row - i * p.hkv.d;
       const int64_t slot = p.slots[i];
+      if constexpr (FSK_WRITE_EARLY) load8<kSrc>(src + i * s_st + h * s_sh, x[u], raw[u]);  // (i < n: in bounds)
       if (slot < 0 || slot >= (int64_t)p.n_slots) continue;
       const uint32_t page = fdiv((uint32_t)slot, p.page);
       const uint32_t r = (uint32_t)slot - page * p.page.d;
-      load8<kSrc>(src + i * s_st + h * s_sh, x[u], raw[u]);
+      if constexpr (!FSK_WRITE_EARLY) load8<kSrc>(src + i * s_st + h * s_sh, x[u], raw[u]);
       doff[u] = page * p_sp + h * p_sh + r * p_st;
     }
 #pragma unroll
