@@ -40,7 +40,7 @@ and B = 1..32 at S=16384), one JSON line per point.
 Other workloads: ``--config C1..C5`` (decode configurations), ``--config M0b``
 (M0 with bf16 Q, KV and output), ``--config G1`` (varlen with sinks at head_dim
 64, Hq=64, Hkv=8), ``--config G2`` (paged at head_dim 256, 16384 tokens per
-sequence), ``--config W0..W2`` (the KV write path: a
+sequence), ``--config W0..W4`` (the KV write path: a
 step is one store of a batch of new rows into scattered pages; ``roofline`` is
 the write kernel).  ``--graph`` replays each decode step from a captured HIP
 graph; ``--block-scores`` also computes the pooled 128-token block scores.
@@ -65,7 +65,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=300,
                     help="untimed steps first (the shader clock takes ~20 ms of load to settle)")
-    ap.add_argument("--config", default="M0", help="workload name (decode: M0, M0b, G1, G2, C1..C5; KV write: W0..W2)")
+    ap.add_argument("--config", default="M0", help="workload name (decode: M0, M0b, G1, G2, C1..C5; KV write: W0..W4)")
     ap.add_argument("--sets", type=int, default=0, help="input sets to rotate (0: >= 4 and enough for > 1.1 GB)")
     ap.add_argument("--chunk", type=int, default=0, help="split size in tokens (0: library default)")
     ap.add_argument("--block-scores", action="store_true",
@@ -86,7 +86,7 @@ def parse():
     ap.add_argument("--traffic", default="",
                     help="rocprof summary holding 'bytes_per_launch: N' for the measured kernel "
                          "(default: profiles/partial_kernel_<config>_traffic.md, or "
-                         "kv_write_kernel_<config>_traffic.md for W0..W2, if committed)")
+                         "kv_write_kernel_<config>_traffic.md for W0..W4, if committed)")
     ap.add_argument("--wave-stamps", action="store_true",
                     help="load the wave-stamp build and print the partial kernel's per-wave timeline "
                          "(start-up, streaming, tail, dispatch) instead of the benchmark line")
@@ -96,6 +96,9 @@ def parse():
     ap.add_argument("--sweep", action="store_true",
                     help="only the reference benchmark's sweep (varlen fp16, lengths U[max(64,S/4), S], "
                          "sinks 0.1 N(0,1), linear fold): S = 512..32768 at B=4, B = 1..32 at S=16384")
+    ap.add_argument("--graph-host", action="store_true",
+                    help="only the host-cost breakdown of graph replays of --config's decode call (torch "
+                         "replay, direct hipGraphLaunch, 10-call graphs, capture modes, first replay)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration under rocprof)")
     return ap.parse_args()
@@ -480,6 +483,74 @@ def wave_timeline(args):
                       "options": args.option, "algorithmic_bytes": base.algorithmic_bytes(), **med}), flush=True)
 
 
+def graph_host(args) -> None:
+    """Where a replayed decode graph's host time goes, for one configuration
+    (--config, default M0; use C1 or C4 for small steps): per decode call,
+    host µs to issue and GPU-bound µs per step, for eager calls, torch's
+    CUDAGraph.replay(), hipGraphLaunch called directly on the same
+    executable graph (ctypes, no torch wrapper), a graph of 10 decode calls,
+    graphs captured in the thread-local and relaxed capture modes, and the
+    first replay after instantiation.  One input set (the host costs are the
+    subject; steps are cache-resident)."""
+    import ctypes
+
+    import torch
+
+    from fasterkernels_amd import workloads as W
+    from fskernels.engine.hip_graph import DecodeGraph
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipGraphLaunch.restype = ctypes.c_int
+    hip.hipGraphLaunch.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    wl = W.make(args.config, gen_device=dev, device=dev)
+    n = max(args.steps, 500)
+
+    def per_call(fn, calls=1):
+        for _ in range(50):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        return {"host_us": round((t1 - t0) / n / calls * 1e6, 2), "gpu_bound_us": round((t2 - t0) / n / calls * 1e6, 2)}
+
+    out = {"graph_host": args.config, "calls": n}
+    out["eager"] = per_call(lambda: W.run(wl))
+    g = DecodeGraph(W.run, wl)
+    out["torch_replay"] = per_call(g.graph.replay)
+    ex, stream = g.graph.raw_cuda_graph_exec(), torch.cuda.current_stream().cuda_stream
+    out["hipGraphLaunch_direct"] = per_call(lambda: hip.hipGraphLaunch(ex, stream))
+
+    def ten():
+        r = None
+        for _ in range(10):
+            r = W.run(wl)
+        return r
+    g10 = DecodeGraph(ten)
+    out["torch_replay_10_calls_per_call"] = per_call(g10.graph.replay, 10)
+    for mode in ("thread_local", "relaxed"):
+        gm = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gm, capture_error_mode=mode):
+            W.run(wl)
+        out[f"torch_replay_capture_{mode}"] = per_call(gm.replay)
+    gf = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gf):
+        W.run(wl)
+    torch.cuda.synchronize()
+    firsts = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        gf.replay()
+        firsts.append(round((time.perf_counter() - t0) * 1e6, 1))
+        torch.cuda.synchronize()
+    out["first_and_second_replay_host_us"] = firsts
+    print(json.dumps(out), flush=True)
+
+
 # Decode configurations timed beside the headline in the default run (the
 # other decode configurations of the benchmark definition).  Each gets its own
 # warm-up and step count, set from elapsed time (the headline keeps the counts
@@ -705,6 +776,9 @@ def main():
         return
     if args.sweep:
         reference_sweep(args)
+        return
+    if args.graph_host:
+        graph_host(args)
         return
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)

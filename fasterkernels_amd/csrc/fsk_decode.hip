@@ -1564,12 +1564,6 @@ constexpr int kWriteThreads = 256;
 #ifndef FSK_WRITE_NT
 #define FSK_WRITE_NT 1
 #endif
-// 1: a thread issues its source-row load together with the slot load (the
-// row's address does not depend on the slot; a skipped token's row is read
-// and dropped), so a step costs one memory round trip instead of two.
-#ifndef FSK_WRITE_EARLY
-#define FSK_WRITE_EARLY 0
-#endif
 constexpr int kWriteUnroll = FSK_WRITE_UNROLL;
 
 template <typename T>
@@ -1695,11 +1689,10 @@ __global__ __launch_bounds__(kWriteThreads) void kv_write_kernel(WriteParams p) 
       const uint32_t i = fdiv(row, p.hkv);
       const uint32_t h = row - i * p.hkv.d;
       const int64_t slot = p.slots[i];
-      if constexpr (FSK_WRITE_EARLY) load8<kSrc>(src + i * s_st + h * s_sh, x[u], raw[u]);  // (i < n: in bounds)
       if (slot < 0 || slot >= (int64_t)p.n_slots) continue;
       const uint32_t page = fdiv((uint32_t)slot, p.page);
       const uint32_t r = (uint32_t)slot - page * p.page.d;
-      if constexpr (!FSK_WRITE_EARLY) load8<kSrc>(src + i * s_st + h * s_sh, x[u], raw[u]);
+      load8<kSrc>(src + i * s_st + h * s_sh, x[u], raw[u]);
       doff[u] = page * p_sp + h * p_sh + r * p_st;
     }
 #pragma unroll

@@ -235,6 +235,11 @@ WRITE_CONFIGS = {
     "W1": dict(src="bf16", pool="e4m3", B=4, L=32768, Hkv=8, D=128, scaled=True, seed=111),
     # one decode step's append: one token for each of C5's 64 sequences
     "W2": dict(src="bf16", pool="e4m3", B=64, L=1, Hkv=8, D=128, scaled=True, seed=112),
+    # W0 and W1 on the pages a fresh PagedKVCache hands out: its LIFO free
+    # list pops page ids downwards, so a prefill of sequence after sequence
+    # gets consecutive pages (descending) instead of W0/W1's shuffled ones
+    "W3": dict(src="f16", pool="f16", B=4, L=32768, Hkv=8, D=128, scaled=False, seed=113, pages="fresh"),
+    "W4": dict(src="bf16", pool="e4m3", B=4, L=32768, Hkv=8, D=128, scaled=True, seed=114, pages="fresh"),
 }
 
 
@@ -262,16 +267,20 @@ class WriteWorkload:
 
 
 def make_write(name: str, *, device, data_seed: int | None = None) -> WriteWorkload:
-    """Rows for sequences of L tokens laid out on a shuffled pool with 10 %
-    spare pages; token t of sequence b goes to its page t // 16, row t % 16."""
+    """Rows for sequences of L tokens laid out on a pool with 10 % spare pages
+    (shuffled, or in a fresh cache's order); token t of sequence b goes to its
+    page t // 16, row t % 16."""
     cfg = WRITE_CONFIGS[name]
     B, L, hkv, d = cfg["B"], cfg["L"], cfg["Hkv"], cfg["D"]
     dev = torch.device(device)
     g = torch.Generator(device=dev).manual_seed(cfg["seed"] if data_seed is None else data_seed)
     pages_per_seq = (L + PAGE - 1) // PAGE
     P = B * pages_per_seq + max(1, B * pages_per_seq // 10)
-    gp = torch.Generator(device=dev).manual_seed(cfg["seed"])
-    perm = torch.randperm(P, device=dev, generator=gp)[:B * pages_per_seq].view(B, pages_per_seq)
+    if cfg.get("pages", "shuffled") == "fresh":
+        perm = (P - 1 - torch.arange(B * pages_per_seq, device=dev)).view(B, pages_per_seq)
+    else:
+        gp = torch.Generator(device=dev).manual_seed(cfg["seed"])
+        perm = torch.randperm(P, device=dev, generator=gp)[:B * pages_per_seq].view(B, pages_per_seq)
     # a decode-step append writes the next row of partly filled pages
     t = torch.arange(L, device=dev) + (7 if L == 1 else 0)
     slots = (perm[:, t // PAGE] * PAGE + t % PAGE).reshape(-1).to(torch.int64)

@@ -463,12 +463,13 @@ def test_rejected_append_leaves_cache_unchanged_and_host_rows_are_copied():
     assert torch.equal(cache.k_pool.cpu(), twin.k_pool.cpu()) and torch.equal(cache.v_pool.cpu(), twin.v_pool.cpu())
 
 
-@pytest.mark.parametrize("name", ["W0", "W1", "W2"])
+@pytest.mark.parametrize("name", ["W0", "W1", "W2", "W3", "W4"])
 def test_bench_write_workloads(name):
     """The bench's KV-write workloads at their bench sizes, bit-exact against
     the oracle: W0 the whole M0 cache (131072 tokens) f16 -> f16, W1 the same
     rows bf16 -> e4m3 with scales, W2 one decode-step append for 64
-    sequences (rows into partly filled pages of a zeroed pool)."""
+    sequences (rows into partly filled pages of a zeroed pool), W3 and W4 as
+    W0 and W1 on a fresh cache's page order."""
     wl = W.make_write(name, device=DEV)
     cfg = W.WRITE_CONFIGS[name]
     W.run_write(wl)
