@@ -75,12 +75,21 @@ def flash_decode_gqa_varlen(q, k, v, cu_seqlens_k, sink=None):
             raise RuntimeError(f"{name} must be a CUDA (HIP) tensor")
     if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError(f"q, k and v must share one of float16 / bfloat16, got {q.dtype}, {k.dtype}, {v.dtype}")
+    # The library reads these tensors through the sizes given here, so their
+    # extents are checked first (a short tensor would be read past its end).
+    if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape or k.shape[2] != q.shape[2]:
+        raise ValueError(f"q must be [B, Hq, D] and k, v [T, Hkv, D], got {tuple(q.shape)}, {tuple(k.shape)}, "
+                         f"{tuple(v.shape)}")
     B, Hq, D = q.shape
     T, Hkv, _ = k.shape
+    if cu_seqlens_k.numel() != B + 1:
+        raise ValueError(f"cu_seqlens_k must have B + 1 = {B + 1} entries, got {cu_seqlens_k.numel()}")
     cu = cu_seqlens_k if (cu_seqlens_k.dtype == torch.int32 and cu_seqlens_k.is_contiguous()) \
         else cu_seqlens_k.to(torch.int32).contiguous()
     if sink is not None:
-        sink = sink.to(device=q.device, dtype=torch.float32).contiguous()
+        if sink.numel() != Hq:
+            raise ValueError(f"sink must have one entry per query head ({Hq}), got {sink.numel()}")
+        sink = sink.to(device=q.device, dtype=torch.float32).reshape(Hq).contiguous()
     out = torch.empty_like(q)
     code = _DTYPES[q.dtype]
     with torch.cuda.device(q.device):  # the size follows the current device's CU count

@@ -75,3 +75,11 @@ def test_reference_binding_errors():
     k96 = torch.zeros(7, 8, 96, dtype=torch.float16, device=DEV)
     with pytest.raises(NotImplementedError):  # head_dim 96: raised, not uninitialised memory
         rb.flash_decode_gqa_varlen(q96, k96, k96, wl.cu_seqlens)
+    # extents the library cannot see are checked before the call
+    sink = torch.zeros(wl.Hq, device=DEV)
+    with pytest.raises(ValueError, match="sink must have one entry per query head"):
+        rb.flash_decode_gqa_varlen(wl.q, wl.k, wl.v, wl.cu_seqlens, sink[:-1])
+    with pytest.raises(ValueError, match="cu_seqlens_k must have B"):
+        rb.flash_decode_gqa_varlen(wl.q, wl.k, wl.v, wl.cu_seqlens[:-1])
+    with pytest.raises(ValueError, match="must be"):  # K rows narrower than q's head_dim
+        rb.flash_decode_gqa_varlen(wl.q, wl.k[..., :64], wl.v[..., :64], wl.cu_seqlens)
