@@ -563,6 +563,21 @@ def test_full_size_constant_values(name):
     assert_close(out, ref, 2e-3, 2e-3, f"{name} with constant V rows")
 
 
+@pytest.mark.parametrize("B,S", [(4, 512), (4, 32768), (32, 16384)])
+def test_reference_sweep_workloads(B, S):
+    """The reference benchmark's own workload as bench.py --sweep measures it
+    (benchmarks/benchmark.py:20-33: lengths uniform in [max(64, S/4), S],
+    sinks 0.1 N(0,1)) through the default entry point, whose linear sink
+    fold is the reference kernels'; the smallest, longest and largest-batch
+    points of the sweep."""
+    wl = W.reference_sweep_workload(B, S)
+    assert wl.B == B and min(wl.lens) >= max(64, S // 4) and max(wl.lens) <= S
+    g = wl.to(DEV)
+    out = dec.flash_decode_gqa_varlen(g.q, g.k, g.v, g.cu_seqlens, g.s_aux)
+    torch.cuda.synchronize()
+    assert_close(out, oracle_for(wl, "linear"), 2e-3, 2e-3, f"reference sweep B={B} S={S}", report=True)
+
+
 @pytest.fixture(scope="module")
 def c5_full():
     return W.make("C5")
