@@ -523,6 +523,9 @@ def graph_host(args) -> None:
     g = DecodeGraph(W.run, wl)
     out["torch_replay"] = per_call(g.graph.replay)
     ex, stream = g.graph.raw_cuda_graph_exec(), torch.cuda.current_stream().cuda_stream
+    st = hip.hipGraphLaunch(ex, stream)
+    if st != 0:
+        raise RuntimeError(f"hipGraphLaunch returned {st}")
     out["hipGraphLaunch_direct"] = per_call(lambda: hip.hipGraphLaunch(ex, stream))
 
     def ten():
