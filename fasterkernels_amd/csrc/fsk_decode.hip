@@ -527,9 +527,12 @@ __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32
   // that differ, at most 8 chunks per sequence.  Then many items hold a
   // boundary, and the lead-ins balance them.  Equal lengths (whose chunks
   // can line up with the sequences) and a few long sequences keep the plain
-  // split, where lead-ins measured slower.
+  // split, where lead-ins measured slower.  Short chunks (no longer than the
+  // lead-in) take lead-ins too, whatever the chunk count: a lead-in of at
+  // least a chunk keeps every item to one sequence's tokens, so no short
+  // item pays a second segment's round trips.
   int X = 0;
-  if (!kScores && p.seg_tokens > 0 && varied && sp.n <= 8 * nonempty) {
+  if (!kScores && p.seg_tokens > 0 && varied && (sp.n <= 8 * nonempty || sp.c_e <= p.seg_tokens)) {
     X = p.seg_tokens;
     total += (uint32_t)(nonempty * X);
     sp = split_geometry(total, sa);

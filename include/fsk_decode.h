@@ -316,9 +316,10 @@ FSK_API int fsk_debug_split(int64_t total, int chunk_min, int chunk_max,
  *                         128..4096, default 2432)
  *   "seg_tokens"          work-stream positions laid before each sequence when
  *                         non-empty lengths differ and there are at most 8
- *                         chunks per sequence, so that items holding a
- *                         sequence boundary carry fewer tokens (multiple of 32
- *                         in 0..256, default 96; 0 = none)
+ *                         chunks per sequence or the chunks are no longer
+ *                         than this, so that items holding a sequence
+ *                         boundary carry fewer tokens (multiple of 32 in
+ *                         0..256, default 96; 0 = none)
  *   "head_pairs"          1 (default): varlen decodes at head_dim 64 with
  *                         packed heads read KV heads 2i and 2i+1 as one
  *                         128-wide row; 0: one KV head per wave
