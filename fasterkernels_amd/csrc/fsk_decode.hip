@@ -54,7 +54,9 @@ static __device__ __align__(256) uint8_t scratch[FSK_NOALLOC_SCRATCH_BYTES];
 // the number of segments it processed [5], its XCC_ID [6] and its HW_ID [7]
 // (wave slot, SIMD, CU, shader array and engine), and for its first item
 // (paged units) when the page window and Q loads are issued [8] and when
-// they have arrived [9].  Vector stores, read back by fsk_debug_wave_stamps.
+// they have arrived [9]; inside the plan, when the lengths are summed [10],
+// after the split [11] and after the lead-in decision (and its second split)
+// [12].  Vector stores, read back by fsk_debug_wave_stamps.
 #ifdef FSK_WAVE_STAMPS
 constexpr int kStampWaves = 4096;
 constexpr int kStampSlots = 16;
@@ -240,7 +242,8 @@ struct Params {
   int pair;                // varlen, head_dim 64: a wave takes KV heads 2i and 2i+1 as one 128-wide row
   int chunk_min, chunk_max;  // split size bounds in tokens (multiples of 32)
   int chunk_pref;          // automatic split: the chunk count doubles while chunks would exceed this
-  int target_units;        // preferred number of sequence chunks per call
+  FastDiv target_div;      // divisor target_units: preferred number of sequence chunks per call
+  FastDiv target_half;     // divisor max(target_units / 2, 1)
   int u_max;               // workspace capacity in units
   int xcd_skew;            // automatic split: long/short chunk pairs for even/odd XCDs, in % (0: equal)
   int seg_tokens;          // stream tokens laid before each non-empty sequence (a multiple of 32)
@@ -340,12 +343,22 @@ __device__ __forceinline__ HalfTile half_tile(const Params& p, int b, int start,
 // and a short one (c_o); c_e == c_o without an XCD skew.  Chunk j starts at
 // (j / 2) * (c_e + c_o) + (j odd ? c_e : 0).
 struct Split {
-  int c_e, c_o, pair;  // pair = c_e + c_o
+  int c_e, c_o, pair;  // pair = c_e + c_o = twice the split's base chunk
   int n;               // chunks in the call
   int paired;          // items map even chunks to even XCDs (see item_of)
+  uint32_t m;          // ceil(2^32 / (pair / 2)): see div_m
 };
+// floor(x / d) for x < 2^31 from m = ceil(2^32 / d): the high word of x m
+// exceeds x / d by less than x / 2^32 < 1/2, so it is floor(x / d) or one
+// more, and one multiply-compare settles which.  (A long division is ~20
+// dependent instructions; this is four.)
+__host__ __device__ __forceinline__ uint32_t div_m(uint32_t x, uint32_t d, uint32_t m) {
+  const uint32_t q = (uint32_t)(((uint64_t)x * m) >> 32);
+  return q - (q * d > x ? 1u : 0u);
+}
 __host__ __device__ __forceinline__ int chunk_of(const Split& sp, int x) {  // x >= 0
-  const int q = (int)((uint32_t)x / (uint32_t)sp.pair);
+  const uint32_t half = (uint32_t)sp.pair >> 1;
+  const int q = (int)(div_m((uint32_t)x, half, sp.m) >> 1);  // floor(x / pair)
   return 2 * q + (x - q * sp.pair >= sp.c_e ? 1 : 0);
 }
 __host__ __device__ __forceinline__ int chunk_lo(const Split& sp, int j) { return (j >> 1) * sp.pair + (j & 1) * sp.c_e; }
@@ -386,12 +399,23 @@ constexpr int kShortChunk = 64;     // smallest automatic split of a short strea
 struct SplitArgs {
   int chunk_min, chunk_max;  // split size bounds in tokens (multiples of align)
   int chunk_pref;            // chunk_min <= chunk_pref <= chunk_max: see the doublings below
-  int target_units;          // preferred number of chunks
+  FastDiv target;            // divisor target_units (<= 2^20): preferred number of chunks
+  FastDiv target_half;       // divisor max(target_units / 2, 1)
   int u_max, B;              // workspace capacity in partials, sequences
   int xcd_skew;              // percent, 0: equal chunks
   int NH;                    // head slots per chunk (work items = chunks x NH)
   int align;
 };
+// ceil(x / (d 2^k)) = ceil(ceil(x / 2^k) / d), for x < 2^31 and k <= 25.
+__host__ __device__ __forceinline__ uint32_t cdiv_shift(uint32_t x, uint32_t k, FastDiv d) {
+  const uint32_t y = (x + (1u << k) - 1) >> k;
+  return y == 0 ? 0u : fdiv(y - 1, d) + 1;
+}
+// Every workgroup runs this on its critical path before its first K/V load,
+// where each dependent instruction costs a few cycles: the divisors are the
+// host's multiply-shift pairs, the comparisons with ceil(x / c) are products
+// (ceil(x / c) > t exactly when x > t c), and one division gives the chunk's
+// reciprocal, which the chunk count, the skewed pairs and chunk_of share.
 __host__ __device__ __forceinline__ Split split_geometry(uint32_t total, const SplitArgs& a) {
   auto cdiv = [](uint32_t x, uint32_t y) { return (x + y - 1) / y; };
   auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
@@ -401,14 +425,13 @@ __host__ __device__ __forceinline__ Split split_geometry(uint32_t total, const S
   // above chunk_pref, then doubled while it would need chunks above
   // chunk_max (a batch too long for target_units chunks gets twice as many
   // rather than a count that leaves some CUs one item short).
-  // cdiv(total, t) > c exactly when t < cdiv(total, c).
+  // target = target_units << k.
   const uint32_t chunk_max = (uint32_t)a.chunk_max;
-  const uint32_t t_need = cdiv(total, chunk_max);
-  uint32_t target = (uint32_t)a.target_units;
-  if (target < cdiv(total, (uint32_t)a.chunk_pref)) target *= 2;
-  while (target < t_need && target < (1u << 24)) target *= 2;
+  uint32_t target = a.target.d, k = 0;
+  if ((uint64_t)target * (uint32_t)a.chunk_pref < total) target *= 2, k = 1;
+  while ((uint64_t)target * chunk_max < total && target < (1u << 24)) target *= 2, ++k;
   auto up = [&](uint32_t x) { return (x + align - 1) / align * align; };
-  uint32_t want = cdiv(total, target);
+  uint32_t want = cdiv_shift(total, k, a.target);  // ceil(total / target)
   uint32_t lo = (uint32_t)a.chunk_min, hi = chunk_max;
   if (want < lo && a.chunk_min < a.chunk_max) {
     // A short stream (target chunks would be below chunk_min): half as many
@@ -417,21 +440,27 @@ __host__ __device__ __forceinline__ Split split_geometry(uint32_t total, const S
     // trips each) and 1-tile items (per-item costs).  Only while that keeps
     // to 32 chunks per sequence on average: the reduce merges 32 partials of
     // a sequence per memory round trip (head_dim 128).
-    const uint32_t w2 = cdiv(total, umax(target / 2, 1u));
+    // w2 = ceil(total / max(target / 2, 1))
+    const uint32_t w2 = k > 0 ? cdiv_shift(total, k - 1, a.target) : cdiv_shift(total, 0, a.target_half);
     const uint32_t lo2 = up((uint32_t)kShortChunk), hi2 = umax((uint32_t)a.chunk_min, lo2);
-    if (cdiv(total, umin(umax(up(w2), lo2), hi2)) <= 32u * (uint32_t)a.B) {
+    const uint32_t c2 = umin(umax(up(w2), lo2), hi2);
+    if ((uint64_t)total <= (uint64_t)32 * (uint32_t)a.B * c2) {
       want = w2;
       lo = lo2;
       hi = hi2;
     }
   }
   uint32_t chunk = umin(umax(up(want), lo), hi);
-  // at most `cap` chunks: every partial must fit the workspace
+  // at most `cap` chunks: every partial must fit the workspace (chunk is a
+  // multiple of align, so only a stream longer than cap chunks moves it)
   const uint32_t cap = a.u_max > a.B + 1 ? (uint32_t)(a.u_max - a.B - 1) : 0;
-  chunk = cap > 0 ? umin(umax(chunk, up(cdiv(total, cap))), chunk_max) : chunk_max;
+  if (cap == 0) chunk = chunk_max;
+  else if ((uint64_t)total > (uint64_t)cap * chunk) chunk = umin(umax(chunk, up(cdiv(total, cap))), chunk_max);
   Split sp;
+  sp.m = 0xFFFFFFFFu / chunk + 1;  // ceil(2^32 / chunk): chunk >= 32
+  const uint32_t whole = div_m(total, chunk, sp.m);  // floor(total / chunk)
   sp.c_e = sp.c_o = (int)chunk;
-  sp.n = (int)cdiv(total, chunk);
+  sp.n = (int)(whole + (whole * chunk != total ? 1 : 0));
   sp.paired = 0;
   if (a.xcd_skew > 0 && chunk >= (uint32_t)kSkewMinChunk && total > 0) {
     // long chunks (1 + skew %) for the even XCDs, short ones for the odd
@@ -439,7 +468,7 @@ __host__ __device__ __forceinline__ Split split_geometry(uint32_t total, const S
     uint32_t ce = (chunk * (uint32_t)(100 + a.xcd_skew) / 100 + align - 1) / align * align;
     ce = umin(ce, chunk_max);
     const uint32_t co = 2 * chunk - ce;
-    const uint32_t q = total / (2 * chunk), r = total - q * 2 * chunk;
+    const uint32_t q = whole >> 1, r = total - q * 2 * chunk;  // pairs of 2 chunk tokens
     uint32_t n = 2 * q + (r > 0 ? 1 : 0) + (r > ce ? 1 : 0);
     n += n & 1;  // even: a trailing chunk past the stream has no tokens
     if (co >= align && co < ce && n <= cap && ((int64_t)n * a.NH) % 8 == 0) {
@@ -521,8 +550,11 @@ __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32
   }
   total = (uint32_t)uniform((int)total);
   nonempty = uniform(nonempty);
-  const SplitArgs sa{p.chunk_min, p.chunk_max, p.chunk_pref, p.target_units, p.u_max, p.B, p.xcd_skew, p.n_items_h, kAlign};
+  FSK_STAMP(10);
+  const SplitArgs sa{p.chunk_min, p.chunk_max, p.chunk_pref, p.target_div, p.target_half, p.u_max, p.B, p.xcd_skew,
+                     p.n_items_h, kAlign};
   Split sp = split_geometry(total, sa);
+  FSK_STAMP(11);
   // Lead-ins where sequence boundaries are common and fall anywhere: lengths
   // that differ, at most 8 chunks per sequence.  Then many items hold a
   // boundary, and the lead-ins balance them.  Equal lengths (whose chunks
@@ -538,11 +570,13 @@ __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32
     sp = split_geometry(total, sa);
   }
   seg_out = X;
+  FSK_STAMP(12);
   sp.c_e = uniform(sp.c_e);
   sp.c_o = uniform(sp.c_o);
   sp.pair = sp.c_e + sp.c_o;
   sp.n = uniform(sp.n);
   sp.paired = uniform(sp.paired);
+  sp.m = (uint32_t)uniform((int)sp.m);
 
   int carry_f = 0, carry_u = 0;
   for (int b0 = 0; b0 < p.B; b0 += kWave) {
@@ -2128,7 +2162,8 @@ int run_decode(const Common& c) {
   p.n_items_h = pair ? c.Hkv / 2 : c.Hkv * n_hb;
   p.nh_div = make_fastdiv((uint32_t)p.n_items_h);
   p.chunk_min = sp.chunk_min; p.chunk_max = sp.chunk_max; p.chunk_pref = sp.chunk_pref;
-  p.target_units = sp.target_units;
+  p.target_div = make_fastdiv((uint32_t)sp.target_units);
+  p.target_half = make_fastdiv((uint32_t)std::max(sp.target_units / 2, 1));
   // The skew is not applied to a fixed split, nor at head_dim 256: there the
   // even and odd XCDs stream at the same rate (16-bit KV: partial kernel
   // 3-4 % slower with it, paged and varlen; e4m3: no difference).
@@ -2685,10 +2720,12 @@ int fsk_debug_split(int64_t total, int chunk_min, int chunk_max, int chunk_pref,
     return fail(FSK_ERR_INVALID, "chunk bounds must be multiples of align with 32 <= chunk_min <= chunk_max");
   if (chunk_pref < chunk_min || chunk_pref > chunk_max)
     return fail(FSK_ERR_INVALID, "chunk_pref must lie in [chunk_min, chunk_max]");
-  if (target_units < 1 || u_max < 0 || u_max >= ((int64_t)1 << 31) || batch < 0 || xcd_skew < 0 || xcd_skew > 50 ||
+  if (target_units < 1 || target_units > (1 << 20) || u_max < 0 || u_max >= ((int64_t)1 << 31) || batch < 0 || xcd_skew < 0 || xcd_skew > 50 ||
       head_slots < 1 || head_slots > (1 << 16))
     return fail(FSK_ERR_INVALID, "bad split arguments");
-  const SplitArgs a{chunk_min, chunk_max, chunk_pref, target_units, (int)u_max, batch, xcd_skew, head_slots, align};
+  const SplitArgs a{chunk_min,  chunk_max, chunk_pref, make_fastdiv((uint32_t)target_units),
+                    make_fastdiv((uint32_t)std::max(target_units / 2, 1)), (int)u_max, batch, xcd_skew, head_slots,
+                    align};
   const Split sp = split_geometry((uint32_t)total, a);
   geometry[0] = sp.c_e;
   geometry[1] = sp.c_o;

@@ -225,3 +225,80 @@ def test_split_random_policies():
         else:
             seen_plain += 1
     assert seen_paired > 100 and seen_plain > 100
+
+
+def split_model(total, cmin, cmax, cpref, target_units, u_max, B, skew, NH, align):
+    """The split policy in plain integer arithmetic (Python's unbounded ints,
+    real divisions): the chunk count target (doubled once past chunk_pref,
+    then while chunks would exceed chunk_max, up to 2^24), the short-stream
+    halving, the workspace cap and the XCD-skewed long/short pairs.  The
+    device computes the same choice with multiply-shift divisors and a
+    chunk reciprocal; this states it without them."""
+    up = lambda x: cdiv(x, align) * align  # noqa: E731
+    target = target_units
+    if target < cdiv(total, cpref):
+        target *= 2
+    while target < cdiv(total, cmax) and target < (1 << 24):
+        target *= 2
+    want, lo, hi = cdiv(total, target), cmin, cmax
+    if want < lo and cmin < cmax:
+        w2 = cdiv(total, max(target // 2, 1))
+        lo2 = up(SHORT_CHUNK)
+        hi2 = max(cmin, lo2)
+        if cdiv(total, min(max(up(w2), lo2), hi2)) <= 32 * B:
+            want, lo, hi = w2, lo2, hi2
+    chunk = min(max(up(want), lo), hi)
+    cap = u_max - B - 1 if u_max > B + 1 else 0
+    chunk = min(max(chunk, up(cdiv(total, cap))), cmax) if cap > 0 else cmax
+    geo = (chunk, chunk, cdiv(total, chunk), 0)
+    if skew > 0 and chunk >= SKEW_MIN and total > 0:
+        ce = min(up(chunk * (100 + skew) // 100), cmax)
+        co = 2 * chunk - ce
+        q, r = divmod(total, 2 * chunk)
+        n = 2 * q + (r > 0) + (r > ce)
+        n += n & 1
+        if align <= co < ce and n <= cap and (n * NH) % 8 == 0:
+            geo = (ce, co, n, 1)
+    return geo
+
+
+def test_split_matches_the_policy_model():
+    """The device's division-free split gives exactly split_model's choice:
+    every policy the host sets (as in test_split_random_policies) and
+    arbitrary argument sets within the entry point's bounds, including
+    streams near 2^31 tokens, odd target counts and workspace caps that
+    bind."""
+    lib = nat.load()
+    geo = (ctypes.c_int32 * 4)()
+    r = np.random.default_rng(11)
+    cases = []
+    for _ in range(3000):
+        align = int(r.choice([32, 128]))
+        B = int(r.choice([1, 4, 32, 64, 65, int(r.integers(1, 5000))]))
+        total = int(r.choice([r.integers(0, 5000), r.integers(0, 1 << 20), r.integers(0, (1 << 31) - 4097)]))
+        total = cdiv(total, align) * align if r.random() < 0.8 else total
+        NH = int(r.choice([1, 3, 4, 8, 16, int(r.integers(1, 1 << 16))]))
+        cus = int(r.choice([1, 32, 80, 256, 304]))
+        fixed = int(r.choice([0, 0, 0, align, 2 * align, 1024 // align * align, 4096]))
+        skew = int(r.choice([0, 3, 6, 20, 50]))
+        pol = list(host_policy(total, B, NH, cus, fixed, skew, most=int(r.choice([0, 0, 64, 512])) // align * align))
+        if pol[0] % align or pol[1] % align or pol[2] % align:
+            continue
+        cases.append((total, *pol[:5], B, pol[5], NH, align))
+    for _ in range(3000):
+        align = int(r.choice([32, 128]))
+        cmin = align * int(r.integers(1, 9))
+        cmax = max(cmin, int(r.choice([cmin, cmin * int(r.integers(1, 40)), 4096 // align * align,
+                                       (1 << int(r.integers(7, 25))) // align * align])))
+        cpref = align * int(r.integers(cmin // align, cmax // align + 1))
+        tu = int(r.choice([1, 2, 3, 5, 7, 64, 85, 128, 341, int(r.integers(1, (1 << 20) + 1))]))
+        B = int(r.choice([0, 1, 4, 64, 200, int(r.integers(0, 5000))]))
+        u_max = int(r.choice([0, B + 1, B + 2, int(r.integers(0, 100_000)), (1 << 31) - 1]))
+        total = int(r.choice([r.integers(0, 4096), r.integers(0, 1 << 20), r.integers(0, (1 << 31) - 4097),
+                              tu * cpref, tu * cpref + 1, tu * cmax, (1 << 31) - 4097]))
+        total = min(total, (1 << 31) - 4097)
+        cases.append((total, cmin, cmax, cpref, tu, u_max, B, int(r.choice([0, 3, 10, 50])),
+                      int(r.choice([1, 4, 8, int(r.integers(1, 1 << 16))])), align))
+    for args in cases:
+        nat.check(lib.fsk_debug_split(*args, geo, None, None, None, None))
+        assert tuple(geo) == split_model(*args), args
