@@ -442,12 +442,11 @@ def wave_timeline(args):
             "waves": int(len(st)), "working_waves": int(work.sum()),
             "start_spread_us": float(us(0).max()),
             "plan_us_after_wave_start": float(np.median((st[:, 1] - st[:, 0]) * 0.01)),
-            # the plan's stages: lengths loaded and summed, the split, the
-            # lead-in decision (with its second split where taken), the prefix tables
+            # the plan's stages: lengths loaded and summed, the split (with
+            # the lead-in decision), the prefix tables
             "plan_lengths_us": float(np.median((st[:, 10] - st[:, 0]) * 0.01)),
             "plan_split_us": float(np.median((st[:, 11] - st[:, 10]) * 0.01)),
-            "plan_leadin_us": float(np.median((st[:, 12] - st[:, 11]) * 0.01)),
-            "plan_prefix_us": float(np.median((st[:, 1] - st[:, 12]) * 0.01)),
+            "plan_prefix_us": float(np.median((st[:, 1] - st[:, 11]) * 0.01)),
             # paged: first item's set-up after the plan, its page window + Q round trip, then its first tiles
             "item_setup_us": med(((st[:, 8] - st[:, 1]) * 0.01)[work & (st[:, 8] > 0)]),
             "window_round_trip_us": med(((st[:, 9] - st[:, 8]) * 0.01)[work & (st[:, 9] > 0)]),

@@ -54,9 +54,9 @@ static __device__ __align__(256) uint8_t scratch[FSK_NOALLOC_SCRATCH_BYTES];
 // the number of segments it processed [5], its XCC_ID [6] and its HW_ID [7]
 // (wave slot, SIMD, CU, shader array and engine), and for its first item
 // (paged units) when the page window and Q loads are issued [8] and when
-// they have arrived [9]; inside the plan, when the lengths are summed [10],
-// after the split [11] and after the lead-in decision (and its second split)
-// [12].  Vector stores, read back by fsk_debug_wave_stamps.
+// they have arrived [9]; inside the plan, when the lengths are summed [10]
+// and when the split (with its lead-in decision) is chosen [11].  Vector
+// stores, read back by fsk_debug_wave_stamps.
 #ifdef FSK_WAVE_STAMPS
 constexpr int kStampWaves = 4096;
 constexpr int kStampSlots = 16;
@@ -215,6 +215,23 @@ __host__ __device__ __forceinline__ uint32_t fdiv(uint32_t x, FastDiv f) {
   return (uint32_t)(((uint64_t)x * f.m) >> f.s);
 }
 
+// The split policy's constants for one call (make_split_args on the host;
+// split_geometry states the policy).  Streams are below 2^31 tokens, so the
+// products with target_units saturate there.
+struct SplitArgs {
+  uint32_t chunk_min, chunk_max;  // split size bounds in tokens (multiples of the padding)
+  uint32_t pref_total;            // min(target_units * chunk_pref, 2^31)
+  uint32_t max_total;             // min(target_units * chunk_max, 2^31)
+  uint32_t short_units;           // min(32 B, 2^32 - 1): most chunks of a short stream's split
+  uint32_t cap;                   // u_max - B - 1 (0: no room): most chunks any split may have
+  FastDiv target;                 // divisor target_units (<= 2^20): preferred number of chunks
+  FastDiv target_half;            // divisor max(target_units / 2, 1)
+  FastDiv cap_div;                // divisor max(cap, 1)
+  uint32_t k_cap;                 // doublings that take target_units to 2^24
+  uint32_t xcd_skew;              // percent (<= 50), 0: equal chunks
+  uint32_t nh7;                   // head slots per chunk, mod 8
+};
+
 // ---------------------------------------------------------------------------
 // Kernel parameters (passed by value)
 // ---------------------------------------------------------------------------
@@ -239,13 +256,11 @@ struct Params {
   int B, Hkv, G, n_hb;
   int n_items_h;           // head slots per chunk: Hkv * n_hb, or Hkv / 2 with pair
   FastDiv nh_div;          // divisor n_items_h
+  FastDiv hb_div;          // divisor n_hb
+  FastDiv hkv_div;         // divisor Hkv
   int pair;                // varlen, head_dim 64: a wave takes KV heads 2i and 2i+1 as one 128-wide row
-  int chunk_min, chunk_max;  // split size bounds in tokens (multiples of 32)
-  int chunk_pref;          // automatic split: the chunk count doubles while chunks would exceed this
-  FastDiv target_div;      // divisor target_units: preferred number of sequence chunks per call
-  FastDiv target_half;     // divisor max(target_units / 2, 1)
+  SplitArgs split;          // the split policy's constants
   int u_max;               // workspace capacity in units
-  int xcd_skew;            // automatic split: long/short chunk pairs for even/odd XCDs, in % (0: equal)
   int seg_tokens;          // stream tokens laid before each non-empty sequence (a multiple of 32)
   int32_t* plan;           // [B+1] unit prefix offsets
   float* part_ml;          // [u_max, Hkv, G, 2]
@@ -394,90 +409,77 @@ constexpr int kShortChunk = 64;     // smallest automatic split of a short strea
 
 // The scalar part of the plan: the chunk geometry of a stream of `total`
 // padded tokens (align = the padding, 32 or 128).  Compiled for the host too,
-// so that the split's invariants can be checked without a GPU
-// (fsk_debug_split).
-struct SplitArgs {
-  int chunk_min, chunk_max;  // split size bounds in tokens (multiples of align)
-  int chunk_pref;            // chunk_min <= chunk_pref <= chunk_max: see the doublings below
-  FastDiv target;            // divisor target_units (<= 2^20): preferred number of chunks
-  FastDiv target_half;       // divisor max(target_units / 2, 1)
-  int u_max, B;              // workspace capacity in partials, sequences
-  int xcd_skew;              // percent, 0: equal chunks
-  int NH;                    // head slots per chunk (work items = chunks x NH)
-  int align;
-};
+// so that the split can be checked without a GPU (fsk_debug_split).
+// ceil(x / d) for x < 2^31 (x = 0 included, without a branch).
+__host__ __device__ __forceinline__ uint32_t cdiv_fast(uint32_t x, FastDiv d) {
+  const uint32_t nz = x != 0 ? 1u : 0u;
+  return (fdiv(x - nz, d) + 1) * nz;
+}
 // ceil(x / (d 2^k)) = ceil(ceil(x / 2^k) / d), for x < 2^31 and k <= 25.
 __host__ __device__ __forceinline__ uint32_t cdiv_shift(uint32_t x, uint32_t k, FastDiv d) {
-  const uint32_t y = (x + (1u << k) - 1) >> k;
-  return y == 0 ? 0u : fdiv(y - 1, d) + 1;
+  return cdiv_fast((x + (1u << k) - 1) >> k, d);
+}
+__host__ __device__ __forceinline__ uint32_t clz32(uint32_t x) { return (uint32_t)__builtin_clz(x); }  // x > 0
+__host__ __device__ __forceinline__ uint32_t umulhi32(uint32_t x, uint32_t y) {
+  return (uint32_t)(((uint64_t)x * y) >> 32);
 }
 // Every workgroup runs this on its critical path before its first K/V load,
-// where each dependent instruction costs a few cycles: the divisors are the
-// host's multiply-shift pairs, the comparisons with ceil(x / c) are products
-// (ceil(x / c) > t exactly when x > t c), and one division gives the chunk's
-// reciprocal, which the chunk count, the skewed pairs and chunk_of share.
-__host__ __device__ __forceinline__ Split split_geometry(uint32_t total, const SplitArgs& a) {
-  auto cdiv = [](uint32_t x, uint32_t y) { return (x + y - 1) / y; };
+// where each dependent instruction costs a few cycles: it is branch-free
+// scalar arithmetic (so that two calls interleave, see build_plan), the
+// divisors are the host's multiply-shift pairs, the comparisons with
+// ceil(x / c) are products (ceil(x / c) > t exactly when x > t c), and one
+// division gives the chunk's reciprocal, which the chunk count, the skewed
+// pairs and chunk_of share.
+__host__ __device__ __forceinline__ Split split_geometry(uint32_t total, const SplitArgs& a, uint32_t align) {
   auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
   auto umin = [](uint32_t x, uint32_t y) { return x < y ? x : y; };
-  const uint32_t align = (uint32_t)a.align;
-  // Chunks per call: target_units, doubled once if that would need chunks
-  // above chunk_pref, then doubled while it would need chunks above
-  // chunk_max (a batch too long for target_units chunks gets twice as many
-  // rather than a count that leaves some CUs one item short).
-  // target = target_units << k.
-  const uint32_t chunk_max = (uint32_t)a.chunk_max;
-  uint32_t target = a.target.d, k = 0;
-  if ((uint64_t)target * (uint32_t)a.chunk_pref < total) target *= 2, k = 1;
-  while ((uint64_t)target * chunk_max < total && target < (1u << 24)) target *= 2, ++k;
-  auto up = [&](uint32_t x) { return (x + align - 1) / align * align; };
+  auto up = [&](uint32_t x) { return (x + align - 1) & ~(align - 1); };  // align: a power of two
+  // Chunks per call: target = target_units << k, doubled once if the chunks
+  // would exceed chunk_pref, then while they would exceed chunk_max, up to
+  // 2^24 chunks (a batch too long for target_units chunks gets twice as many
+  // rather than a count that leaves some CUs one item short).  k1: the
+  // fewest doublings with target chunk_max >= total.
+  const uint32_t P = a.max_total;
+  const uint32_t d = P < total ? clz32(P) - clz32(total) : 0u;  // P << d has total's top bit
+  const uint32_t k1 = P < total ? d + ((P << d) < total ? 1u : 0u) : 0u;
+  const uint32_t k = umax(a.pref_total < total ? 1u : 0u, umin(k1, a.k_cap));
   uint32_t want = cdiv_shift(total, k, a.target);  // ceil(total / target)
-  uint32_t lo = (uint32_t)a.chunk_min, hi = chunk_max;
-  if (want < lo && a.chunk_min < a.chunk_max) {
-    // A short stream (target chunks would be below chunk_min): half as many
-    // chunks, of kShortChunk to chunk_min tokens.  Items of 2-3 tiles
-    // finished sooner than both 4-tile items (fewer waves, twice the round
-    // trips each) and 1-tile items (per-item costs).  Only while that keeps
-    // to 32 chunks per sequence on average: the reduce merges 32 partials of
-    // a sequence per memory round trip (head_dim 128).
-    // w2 = ceil(total / max(target / 2, 1))
-    const uint32_t w2 = k > 0 ? cdiv_shift(total, k - 1, a.target) : cdiv_shift(total, 0, a.target_half);
-    const uint32_t lo2 = up((uint32_t)kShortChunk), hi2 = umax((uint32_t)a.chunk_min, lo2);
-    const uint32_t c2 = umin(umax(up(w2), lo2), hi2);
-    if ((uint64_t)total <= (uint64_t)32 * (uint32_t)a.B * c2) {
-      want = w2;
-      lo = lo2;
-      hi = hi2;
-    }
-  }
-  uint32_t chunk = umin(umax(up(want), lo), hi);
-  // at most `cap` chunks: every partial must fit the workspace (chunk is a
-  // multiple of align, so only a stream longer than cap chunks moves it)
-  const uint32_t cap = a.u_max > a.B + 1 ? (uint32_t)(a.u_max - a.B - 1) : 0;
-  if (cap == 0) chunk = chunk_max;
-  else if ((uint64_t)total > (uint64_t)cap * chunk) chunk = umin(umax(chunk, up(cdiv(total, cap))), chunk_max);
+  // A short stream (target chunks would be below chunk_min): half as many
+  // chunks, of kShortChunk to chunk_min tokens.  Items of 2-3 tiles finished
+  // sooner than both 4-tile items (fewer waves, twice the round trips each)
+  // and 1-tile items (per-item costs).  Only while that keeps to 32 chunks
+  // per sequence on average: the reduce merges 32 partials of a sequence per
+  // memory round trip (head_dim 128).
+  const uint32_t lo2 = up((uint32_t)kShortChunk), hi2 = umax(a.chunk_min, lo2);
+  const uint32_t w2 = cdiv_shift(total, k > 0 ? k - 1 : 0u, k > 0 ? a.target : a.target_half);  // ceil(total / max(target / 2, 1))
+  const uint32_t c2 = umin(umax(up(w2), lo2), hi2);
+  const bool fits = umulhi32(a.short_units, c2) != 0 || total <= a.short_units * c2;  // ceil(total / c2) <= 32 B
+  const bool take = want < a.chunk_min && a.chunk_min < a.chunk_max && fits;
+  want = take ? w2 : want;
+  uint32_t chunk = umin(umax(up(want), take ? lo2 : a.chunk_min), take ? hi2 : a.chunk_max);
+  // at most `cap` chunks: every partial must fit the workspace
+  const uint32_t c_cap = up(cdiv_fast(total, a.cap_div));  // up(ceil(total / cap))
+  chunk = a.cap == 0 ? a.chunk_max : umin(umax(chunk, c_cap), a.chunk_max);
   Split sp;
   sp.m = 0xFFFFFFFFu / chunk + 1;  // ceil(2^32 / chunk): chunk >= 32
   const uint32_t whole = div_m(total, chunk, sp.m);  // floor(total / chunk)
-  sp.c_e = sp.c_o = (int)chunk;
-  sp.n = (int)(whole + (whole * chunk != total ? 1 : 0));
-  sp.paired = 0;
-  if (a.xcd_skew > 0 && chunk >= (uint32_t)kSkewMinChunk && total > 0) {
-    // long chunks (1 + skew %) for the even XCDs, short ones for the odd
-    // (short splits are latency-bound: there the longer chunks cost more)
-    uint32_t ce = (chunk * (uint32_t)(100 + a.xcd_skew) / 100 + align - 1) / align * align;
-    ce = umin(ce, chunk_max);
-    const uint32_t co = 2 * chunk - ce;
-    const uint32_t q = whole >> 1, r = total - q * 2 * chunk;  // pairs of 2 chunk tokens
-    uint32_t n = 2 * q + (r > 0 ? 1 : 0) + (r > ce ? 1 : 0);
-    n += n & 1;  // even: a trailing chunk past the stream has no tokens
-    if (co >= align && co < ce && n <= cap && ((int64_t)n * a.NH) % 8 == 0) {
-      sp.c_e = (int)ce;
-      sp.c_o = (int)co;
-      sp.n = (int)n;
-      sp.paired = 1;
-    }
-  }
+  const uint32_t n_eq = whole + (whole * chunk != total ? 1u : 0u);
+  // XCD skew: long chunks (1 + skew %) for the even XCDs, short ones for the
+  // odd, in pairs of 2 chunk tokens (short splits are latency-bound: there
+  // the longer chunks cost more).  The count is even (a trailing chunk past
+  // the stream has no tokens) and the items map onto the XCDs (n NH a
+  // multiple of 8).
+  const uint32_t ce = umin(up(chunk * (100 + a.xcd_skew) / 100), a.chunk_max);
+  const uint32_t co = 2 * chunk - ce;
+  const uint32_t q = whole >> 1, r = total - q * 2 * chunk;
+  uint32_t n_sk = 2 * q + (r > 0 ? 1u : 0u) + (r > ce ? 1u : 0u);
+  n_sk += n_sk & 1;
+  const bool skew = a.xcd_skew > 0 && chunk >= (uint32_t)kSkewMinChunk && total > 0 && co >= align && co < ce &&
+                    n_sk <= a.cap && (((n_sk & 7) * a.nh7) & 7) == 0;
+  sp.c_e = (int)(skew ? ce : chunk);
+  sp.c_o = (int)(skew ? co : chunk);
+  sp.n = (int)(skew ? n_sk : n_eq);
+  sp.paired = skew ? 1 : 0;
   sp.pair = sp.c_e + sp.c_o;
   return sp;
 }
@@ -505,18 +507,16 @@ __device__ __forceinline__ void seq_range_first(const Params& p, int lane, int& 
   if (lane >= p.B) start = len = 0;
 }
 
+// len0: length of sequence `lane` (0 past B), from seq_range_first, whose
+// loads the caller issues first.
 template <int kLayout, bool kScores>
-__device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32_t* flat, int& start0_out,
-                                            int& len0_out, int& seg_out, int& flat0_out, int& pre0_out) {
+__device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32_t* flat, const int len0,
+                                            int& seg_out, int& flat0_out, int& pre0_out) {
   constexpr int kAlign = kScores ? 128 : 32;
   const int lane = threadIdx.x;
   // Lengths of sequences lane, lane + 64, ...; the first block stays in a
   // register so that the common case (B <= 64) reads them once (and the
   // work loop reads them from these registers, not from memory).
-  int len0 = 0, start0 = 0;
-  seq_range_first<kLayout>(p, lane, start0, len0);
-  start0_out = start0;
-  len0_out = len0;
   // The lengths of sequences 64 and up go to the pre[] table first (which
   // the unit prefix overwrites below, each entry after its own lane has read
   // it), four blocks of 64 per memory round trip rather than one.
@@ -551,10 +551,6 @@ __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32
   total = (uint32_t)uniform((int)total);
   nonempty = uniform(nonempty);
   FSK_STAMP(10);
-  const SplitArgs sa{p.chunk_min, p.chunk_max, p.chunk_pref, p.target_div, p.target_half, p.u_max, p.B, p.xcd_skew,
-                     p.n_items_h, kAlign};
-  Split sp = split_geometry(total, sa);
-  FSK_STAMP(11);
   // Lead-ins where sequence boundaries are common and fall anywhere: lengths
   // that differ, at most 8 chunks per sequence.  Then many items hold a
   // boundary, and the lead-ins balance them.  Equal lengths (whose chunks
@@ -562,15 +558,21 @@ __device__ __forceinline__ Split build_plan(const Params& p, int32_t* pre, int32
   // split, where lead-ins measured slower.  Short chunks (no longer than the
   // lead-in) take lead-ins too, whatever the chunk count: a lead-in of at
   // least a chunk keeps every item to one sequence's tokens, so no short
-  // item pays a second segment's round trips.
+  // item pays a second segment's round trips.  The test is made on the split
+  // with lead-ins, so that a call that takes them computes one split (each
+  // costs ~0.4 us of a workgroup's start).
   int X = 0;
-  if (!kScores && p.seg_tokens > 0 && varied && (sp.n <= 8 * nonempty || sp.c_e <= p.seg_tokens)) {
-    X = p.seg_tokens;
-    total += (uint32_t)(nonempty * X);
-    sp = split_geometry(total, sa);
+  Split sp;
+  const uint32_t seg = (uint32_t)p.seg_tokens;
+  if (!kScores && seg > 0 && varied) {
+    sp = split_geometry(total + (uint32_t)nonempty * seg, p.split, kAlign);
+    if (sp.n <= 8 * nonempty || (uint32_t)sp.c_e <= seg) X = (int)seg;
+    else sp = split_geometry(total, p.split, kAlign);
+  } else {
+    sp = split_geometry(total, p.split, kAlign);
   }
+  FSK_STAMP(11);
   seg_out = X;
-  FSK_STAMP(12);
   sp.c_e = uniform(sp.c_e);
   sp.c_o = uniform(sp.c_o);
   sp.pair = sp.c_e + sp.c_o;
@@ -761,9 +763,9 @@ __device__ __forceinline__ HalfTile unit_half(const Params& p, const Unit& un, i
 // well in order; rotated, M0 83.0 -> 83.7 µs and C3 185 -> 188.7 µs), and so
 // do block scores (the running block maximum is stored when a block ends).
 template <int kLayout, bool kScores>
-__device__ __forceinline__ int tile_rotation(int kvh, int n_tiles, int Hkv) {
+__device__ __forceinline__ int tile_rotation(int kvh, int n_tiles, FastDiv hkv) {
   if constexpr (kScores || kLayout == kPaged) return 0;
-  return kvh * n_tiles / Hkv;
+  return (int)fdiv((uint32_t)(kvh * n_tiles), hkv);  // kvh < Hkv, n_tiles <= 128
 }
 
 // Token position of the k-th tile of a unit of n tiles starting at t0 with
@@ -775,14 +777,52 @@ __device__ __forceinline__ int tile_pos(int k, int n, int rot, int t0, int t_end
   return k < n ? t0 + 32 * j : t_end;
 }
 
-template <int D, int kKV, int kLayout>
-__device__ __forceinline__ void issue_tile(TileRegs<D, kKV>& T, uint32_t kstage_off, const Params& p,
-                                           const Unit& un, int t, int g, int c) {
+// Per-lane byte offsets of a tile's loads and of its K-stage reads.  They
+// depend on the lane and the KV row strides only, so a workgroup computes
+// them while its length loads are in flight instead of after its plan, on
+// the way to its first tile loads (each instruction there costs a few
+// cycles of the start-up); the empty asm statements keep the compiler from
+// recomputing them later.
+template <int D, int kKV>
+struct LaneGeo {
   using TR = TileRegs<D, kKV>;
-  constexpr int kElem = TR::kFp8 ? 1 : 2;
+  static constexpr int kReads = TR::kFp8 ? (D / 32 + 1) / 2 : D / 32;  // K chunks a lane reads per half tile
+  int dma[TR::kDma];     // K DMA r: row R = r kRowsPerDma + lane / kChunks, chunk (lane % kChunks) ^ swz(R)
+  int vrow[4];           // V rows 4g + r, this lane's kVBytes of them
+  uint32_t kread[kReads];  // K-stage offset of the chunk of k-step i (e4m3: k-steps 2i, 2i + 1) in row c
+};
+template <int D, int kKV>
+__device__ __forceinline__ LaneGeo<D, kKV> lane_geo(const Params& p, int lane, int g, int c) {
+  using TR = TileRegs<D, kKV>;
+  using LG = LaneGeo<D, kKV>;
   constexpr int kRowsPerDma = 64 / TR::kChunks;
   const int kst = (int)p.k_st, vst = (int)p.v_st;
-  const int lane = threadIdx.x;
+  LG lg;
+#pragma unroll
+  for (int r = 0; r < TR::kDma; ++r) {
+    const int R = r * kRowsPerDma + lane / TR::kChunks;
+    lg.dma[r] = R * kst + 16 * ((lane % TR::kChunks) ^ k_swizzle<TR::kChunks>(R));
+    asm volatile("" : "+v"(lg.dma[r]));
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    lg.vrow[r] = (4 * g + r) * vst + c * TR::kVBytes;
+    asm volatile("" : "+v"(lg.vrow[r]));
+  }
+#pragma unroll
+  for (int i = 0; i < LG::kReads; ++i) {
+    lg.kread[i] = 16 * (c * TR::kChunks + ((4 * i + g) ^ k_swizzle<TR::kChunks>(c)));
+    asm volatile("" : "+v"(lg.kread[i]));
+  }
+  return lg;
+}
+
+template <int D, int kKV, int kLayout>
+__device__ __forceinline__ void issue_tile(TileRegs<D, kKV>& T, uint32_t kstage_off, const Params& p,
+                                           const Unit& un, int t, const LaneGeo<D, kKV>& lg) {
+  using TR = TileRegs<D, kKV>;
+  constexpr int kElem = TR::kFp8 ? 1 : 2;
+  const int kst = (int)p.k_st, vst = (int)p.v_st;
   // The stage is about to be overwritten: keep earlier LDS reads of it before this point.
   asm volatile("" ::: "memory");
 #pragma unroll
@@ -797,14 +837,9 @@ __device__ __forceinline__ void issue_tile(TileRegs<D, kKV>& T, uint32_t kstage_
     // fetches row R = r * kRowsPerDma + L / kChunks, chunk (L % kChunks) ^
     // swz(R); rows past the valid ones read as zero).
 #pragma unroll
-    for (int r = 0; r < TR::kDma; ++r) {
-      const int R = r * kRowsPerDma + lane / TR::kChunks;
-      const int m = lane % TR::kChunks;
-      lds_dma16(rk, kstage_off + h2 * TR::kHalfBytes + r * 1024, R * kst + 16 * (m ^ k_swizzle<TR::kChunks>(R)));
-    }
+    for (int r = 0; r < TR::kDma; ++r) lds_dma16(rk, kstage_off + h2 * TR::kHalfBytes + r * 1024, lg.dma[r]);
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      T.v[4 * h2 + r] = buf_load<TR::kVBytes, kKvAux>(rv, (4 * g + r) * vst + c * TR::kVBytes);
+    for (int r = 0; r < 4; ++r) T.v[4 * h2 + r] = buf_load<TR::kVBytes, kKvAux>(rv, lg.vrow[r]);
   }
 }
 
@@ -831,7 +866,7 @@ struct Softmax {
 template <int D, int kQ, int kKV>
 __device__ __forceinline__ float compute_tile(const TileRegs<D, kKV>& T, uint32_t kstage,
                                               Softmax<D, kQ, kKV>& st, const u32x4 (&qop)[D / 32], float sscale,
-                                              int g, int c) {
+                                              int g, const LaneGeo<D, kKV>& lg) {
   using TR = TileRegs<D, kKV>;
   using SM = Softmax<D, kQ, kKV>;
   constexpr int kSteps = SM::kSteps;
@@ -847,12 +882,12 @@ __device__ __forceinline__ float compute_tile(const TileRegs<D, kKV>& T, uint32_
       u32x4 kop;
       if constexpr (TR::kFp8) {
         // e4m3: chunk 4 (i / 2) + g holds k-steps i and i + 1
-        const u32x4 raw = k_chunk<D, kKV>(kstage, h2, c, 4 * (i >> 1) + g);
+        const u32x4 raw = *(lds_u32x4*)(uintptr_t)(kstage + h2 * TR::kHalfBytes + lg.kread[i >> 1]);
         const u32x2 a = e4m3x4_to<SM::kQkBf16>(raw[2 * (i & 1)]);
         const u32x2 bb = e4m3x4_to<SM::kQkBf16>(raw[2 * (i & 1) + 1]);
         kop = u32x4{a[0], a[1], bb[0], bb[1]};
       } else {
-        kop = k_chunk<D, kKV>(kstage, h2, c, 4 * i + g);
+        kop = *(lds_u32x4*)(uintptr_t)(kstage + h2 * TR::kHalfBytes + lg.kread[i]);
       }
       s[h2] = mfma16x16x32<SM::kQkBf16>(kop, qop[i], s[h2]);
     }
@@ -1104,7 +1139,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   int lane_start, lane_len;  // start and length of sequence `lane` (B <= 64)
   int lane_flat, lane_pre;   // flat[lane] and pre[lane] of the plan (B <= 64)
   int seg_x;  // empty stream positions before each sequence (see build_plan)
-  const Split sp = build_plan<kLayout, kScores>(p, s_pre, s_flat, lane_start, lane_len, seg_x, lane_flat, lane_pre);
+  seq_range_first<kLayout>(p, lane, lane_start, lane_len);  // the wave's first memory requests
+  __builtin_amdgcn_sched_barrier(0);                        // (ahead of any kernel-argument load)
+  // ... and while they are in flight, the lane's tile offsets
+  const LaneGeo<D, kKV> lg = lane_geo<D, kKV>(p, lane, g, c);
+  const Split sp = build_plan<kLayout, kScores>(p, s_pre, s_flat, lane_len, seg_x, lane_flat, lane_pre);
   FSK_STAMP(1);
   int segments_done = 0;
   const int NH = p.n_items_h;
@@ -1128,7 +1167,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   for (int w = blockIdx.x; w < W; w += gridDim.x) {
     int jc, hh;
     item_of(sp, (uint32_t)w, p.nh_div, jc, hh);
-    const int kvh = p.n_hb == 1 ? hh : hh / p.n_hb;  // (with pair: the pair index, n_hb = 1)
+    const int kvh = (int)fdiv((uint32_t)hh, p.hb_div);  // (with pair: the pair index, n_hb = 1)
     const int hb = hh - kvh * p.n_hb;
     const int lo = chunk_lo(sp, jc), hi = lo + chunk_len(sp, jc);  // stream range of this chunk
     // the last sequence whose region starts at or before lo (flat is nondecreasing, flat[0] = 0)
@@ -1257,12 +1296,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
       // conditional issue would make the compiler wait for all loads).
       TR tiles[kDepth];
       const int n_tiles = (un.t_end - un.t_begin + 31) >> 5;
-      const int rot = uniform(tile_rotation<kLayout, kScores>(un.kvh, n_tiles, p.Hkv));
+      const int rot = uniform(tile_rotation<kLayout, kScores>(un.kvh, n_tiles, p.hkv_div));
       int k = 0;  // tiles computed so far
 #pragma unroll
       for (int s = 0; s < kDepth - 1; ++s)
         issue_tile<D, kKV, kLayout>(tiles[s], s_kstage + s * 2 * TR::kHalfBytes, p, un,
-                                    tile_pos(s, n_tiles, rot, un.t_begin, un.t_end), g, c);
+                                    tile_pos(s, n_tiles, rot, un.t_begin, un.t_end), lg);
       bool done = false;
       while (!done) {
 #pragma unroll
@@ -1270,14 +1309,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
           if (!done) {
             const int tn = tile_pos(k + kDepth - 1, n_tiles, rot, un.t_begin, un.t_end);
             const int sn = (s + kDepth - 1) % kDepth;
-            issue_tile<D, kKV, kLayout>(tiles[sn], s_kstage + sn * 2 * TR::kHalfBytes, p, un, tn, g, c);
+            issue_tile<D, kKV, kLayout>(tiles[sn], s_kstage + sn * 2 * TR::kHalfBytes, p, un, tn, lg);
             wait_k_stage<TR::kLoads, kDepth>(kDepth - 1);
             if (k == 0 && segments_done == 0) FSK_STAMP(2);
             if constexpr (kValu) {
               compute_tile_valu<D>(tiles[s], s_kstage + s * 2 * TR::kHalfBytes, sv, qv, sscale, g, c);
             } else {
               const float mt = compute_tile<D, kQ, kKV>(tiles[s], s_kstage + s * 2 * TR::kHalfBytes, st, qop,
-                                                        sscale, g, c);
+                                                        sscale, g, lg);
               if constexpr (kScores) bm.add(p, un, un.t_begin + 32 * k, mt, head, head_ok, g);
             }
             ++k;
@@ -1288,13 +1327,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
     } else {
       TR ta;
       for (int t = un.t_begin; t < un.t_end; t += 32) {
-        issue_tile<D, kKV, kLayout>(ta, s_kstage, p, un, t, g, c);
+        issue_tile<D, kKV, kLayout>(ta, s_kstage, p, un, t, lg);
         wait_k_stage<TR::kLoads, 1>(0);
         if (t == un.t_begin && segments_done == 0) FSK_STAMP(2);
         if constexpr (kValu) {
           compute_tile_valu<D>(ta, s_kstage, sv, qv, sscale, g, c);
         } else {
-          const float mt = compute_tile<D, kQ, kKV>(ta, s_kstage, st, qop, sscale, g, c);
+          const float mt = compute_tile<D, kQ, kKV>(ta, s_kstage, st, qop, sscale, g, lg);
           if constexpr (kScores) bm.add(p, un, t, mt, head, head_ok, g);
         }
       }
@@ -2119,6 +2158,29 @@ FastDiv make_fastdiv(uint32_t d) {
   return FastDiv{d, (uint32_t)((two_s + d - 1) / d), 31 + l};
 }
 
+// The split policy's per-call constants (see SplitArgs): target_units <=
+// 2^20, chunk bounds <= 2^24, 0 <= u_max < 2^31.
+SplitArgs make_split_args(int chunk_min, int chunk_max, int chunk_pref, int target_units, int64_t u_max, int B,
+                          int xcd_skew, int head_slots) {
+  SplitArgs a;
+  const uint64_t lim = (uint64_t)1 << 31;
+  a.chunk_min = (uint32_t)chunk_min;
+  a.chunk_max = (uint32_t)chunk_max;
+  a.pref_total = (uint32_t)std::min<uint64_t>((uint64_t)target_units * (uint64_t)chunk_pref, lim);
+  a.max_total = (uint32_t)std::min<uint64_t>((uint64_t)target_units * (uint64_t)chunk_max, lim);
+  a.short_units = (uint32_t)std::min<uint64_t>(32 * (uint64_t)std::max(B, 0), 0xFFFFFFFFull);
+  const int64_t cap = u_max > (int64_t)B + 1 ? u_max - B - 1 : 0;
+  a.cap = (uint32_t)cap;
+  a.target = make_fastdiv((uint32_t)target_units);
+  a.target_half = make_fastdiv((uint32_t)std::max(target_units / 2, 1));
+  a.cap_div = make_fastdiv((uint32_t)std::max<int64_t>(cap, 1));
+  a.k_cap = 0;
+  while (((uint64_t)target_units << a.k_cap) < ((uint64_t)1 << 24)) ++a.k_cap;
+  a.xcd_skew = (uint32_t)xcd_skew;
+  a.nh7 = (uint32_t)head_slots & 7;
+  return a;
+}
+
 int run_decode(const Common& c) {
   int st = validate(c);
   if (st != FSK_OK) return st;
@@ -2161,13 +2223,14 @@ int run_decode(const Common& c) {
   p.pair = pair ? 1 : 0;
   p.n_items_h = pair ? c.Hkv / 2 : c.Hkv * n_hb;
   p.nh_div = make_fastdiv((uint32_t)p.n_items_h);
-  p.chunk_min = sp.chunk_min; p.chunk_max = sp.chunk_max; p.chunk_pref = sp.chunk_pref;
-  p.target_div = make_fastdiv((uint32_t)sp.target_units);
-  p.target_half = make_fastdiv((uint32_t)std::max(sp.target_units / 2, 1));
+  p.hb_div = make_fastdiv((uint32_t)p.n_hb);
+  p.hkv_div = make_fastdiv((uint32_t)c.Hkv);
   // The skew is not applied to a fixed split, nor at head_dim 256: there the
   // even and odd XCDs stream at the same rate (16-bit KV: partial kernel
   // 3-4 % slower with it, paged and varlen; e4m3: no difference).
-  p.xcd_skew = (sp.chunk_min == sp.chunk_max || c.D > 128) ? 0 : g_opt.xcd_skew;
+  const int xcd_skew = (sp.chunk_min == sp.chunk_max || c.D > 128) ? 0 : g_opt.xcd_skew;
+  p.split = make_split_args(sp.chunk_min, sp.chunk_max, sp.chunk_pref, sp.target_units, u_max, c.B, xcd_skew,
+                            p.n_items_h);
   p.seg_tokens = g_opt.seg_tokens;
   p.u_max = (int)u_max;
   uint8_t* ws = (uint8_t*)c.ws;
@@ -2723,10 +2786,9 @@ int fsk_debug_split(int64_t total, int chunk_min, int chunk_max, int chunk_pref,
   if (target_units < 1 || target_units > (1 << 20) || u_max < 0 || u_max >= ((int64_t)1 << 31) || batch < 0 || xcd_skew < 0 || xcd_skew > 50 ||
       head_slots < 1 || head_slots > (1 << 16))
     return fail(FSK_ERR_INVALID, "bad split arguments");
-  const SplitArgs a{chunk_min,  chunk_max, chunk_pref, make_fastdiv((uint32_t)target_units),
-                    make_fastdiv((uint32_t)std::max(target_units / 2, 1)), (int)u_max, batch, xcd_skew, head_slots,
-                    align};
-  const Split sp = split_geometry((uint32_t)total, a);
+  const SplitArgs a =
+      make_split_args(chunk_min, chunk_max, chunk_pref, target_units, u_max, batch, xcd_skew, head_slots);
+  const Split sp = split_geometry((uint32_t)total, a, (uint32_t)align);
   geometry[0] = sp.c_e;
   geometry[1] = sp.c_o;
   geometry[2] = sp.n;
