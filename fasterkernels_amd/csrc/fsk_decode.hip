@@ -1699,7 +1699,7 @@ __device__ __forceinline__ float div_by_scale(float x, double rs) {
 // (rs = 1 / scale in binary64, see div_by_scale) and clamped to +-448 (the
 // quantiser of fskernels/triton/triton_gqa_decode_hf_fp8.py:13-16); without one
 // they are cast as they are, so magnitudes above 464 encode NaN as the cast
-// does.  NaN inputs give 0x7F with the input's sign bit, as the cast does.
+// does.  NaN inputs are left to nan_codes.
 template <bool kScaled>
 __device__ __forceinline__ uint32_t encode_e4m3x4(const float* x, double rs) {
   float y[4];
@@ -1710,7 +1710,11 @@ __device__ __forceinline__ uint32_t encode_e4m3x4(const float* x, double rs) {
   }
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w, true);
-  uint32_t u = (uint32_t)w;
+  return (uint32_t)w;
+}
+
+// NaN inputs take 0x7F with the input's sign bit, as torch's cast gives them.
+__device__ __forceinline__ uint32_t nan_codes(uint32_t u, const float* x) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     if (x[j] != x[j]) {
@@ -1776,7 +1780,17 @@ __global__ __launch_bounds__(kWriteThreads) void kv_write_kernel(WriteParams p) 
       if (doff[u] < 0) continue;
       uint8_t* dst = pool + doff[u];
       if constexpr (kPool == kE4M3) {
-        row_store((u32x2*)dst, u32x2{encode_e4m3x4<kScaled>(x[u], rscale), encode_e4m3x4<kScaled>(x[u] + 4, rscale)});
+        u32x2 codes{encode_e4m3x4<kScaled>(x[u], rscale), encode_e4m3x4<kScaled>(x[u] + 4, rscale)};
+        // The NaN fix-up only where the wave holds a NaN: the quantising
+        // write is VALU-bound enough that per-code selects cost it ~2 %.
+        bool nan = false;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) nan = nan || x[u][j] != x[u][j];
+        if (__builtin_amdgcn_ballot_w64(nan) != 0) {
+          codes[0] = nan_codes(codes[0], x[u]);
+          codes[1] = nan_codes(codes[1], x[u] + 4);
+        }
+        row_store((u32x2*)dst, codes);
       } else if constexpr (kPool == kSrc) {
         row_store((u32x4*)dst, raw[u]);  // same type: a bit-exact copy
       } else {
