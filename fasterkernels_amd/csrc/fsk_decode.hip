@@ -353,7 +353,8 @@ __device__ __forceinline__ HalfTile half_tile(const Params& p, int b, int start,
 // total); lane b also returns its own entries flat[b] and pre[b] (the work
 // loop reads them from registers when B <= 64).  Workgroup 0 publishes pre
 // for the reduce kernel.  Every workgroup computes the same plan from the
-// same lengths.  Returns the chunk count.
+// same lengths (split_geometry has the exact rule, with a short-stream case).
+// build_plan returns the split.
 // Chunk geometry.  The stream is cut into pairs of a long chunk (c_e tokens)
 // and a short one (c_o); c_e == c_o without an XCD skew.  Chunk j starts at
 // (j / 2) * (c_e + c_o) + (j odd ? c_e : 0).
