@@ -1619,7 +1619,8 @@ struct WriteParams {
   uint32_t n_slots;                    // num_pages * page_size (< 2^31)
   uint32_t rows;                       // n * Hkv
   FastDiv hkv, page;                   // divisors Hkv and page_size
-  int groups;                          // D / 8 column groups per row
+  FastDiv groups;                      // divisor D / 8: column groups per row
+  uint32_t rows_per_block;             // kWriteThreads / groups
   int32_t* bt;                         // block-table updates: bt[upd[2j]] = upd[2j+1]
   int64_t bt_numel;
   const int64_t* upd;
@@ -1627,21 +1628,17 @@ struct WriteParams {
 };
 
 constexpr int kWriteThreads = 256;
-// Rows per thread per step (loads issued before stores), workgroups per CU
-// for each of the K and V planes, and the cache policy of the row loads and
-// stores (1: non-temporal, each row is read once and written once).  One row
-// per step with non-temporal access measured fastest (W0 206.5 -> 199.7 us,
-// W1 162.3 -> 155.1 us against 4 rows and the default policy).
-#ifndef FSK_WRITE_UNROLL
-#define FSK_WRITE_UNROLL 1
-#endif
+// Workgroups per CU for each of the K and V planes, and the cache policy of
+// the row loads and stores (1: non-temporal, each row is read once and
+// written once).  A thread stores one row per step; with non-temporal access
+// that measured fastest (W0 206.5 -> 199.7 us, W1 162.3 -> 155.1 us against
+// four rows loaded before their stores and the default policy).
 #ifndef FSK_WRITE_BLOCKS_PER_CU
 #define FSK_WRITE_BLOCKS_PER_CU 16
 #endif
 #ifndef FSK_WRITE_NT
 #define FSK_WRITE_NT 1
 #endif
-constexpr int kWriteUnroll = FSK_WRITE_UNROLL;
 
 template <typename T>
 __device__ __forceinline__ T row_load(const T* p) {
@@ -1654,28 +1651,51 @@ __device__ __forceinline__ void row_store(T* p, T x) {
   else *p = x;
 }
 
+// One thread's share of a row in flight: its slot and its 8 source elements
+// (raw bits; f32 sources in two halves).
+struct WriteRow {
+  int64_t slot;
+  uint32_t i, h;  // token and head of the row
+  u32x4 raw[2];
+};
+
+// Issues the loads of row `row` (< rows): the slot and the source elements
+// together, so a row costs one memory round trip before its store.
 template <int kSrc>
-__device__ __forceinline__ void load8(const uint8_t* p, float (&x)[8], u32x4& raw) {
+__device__ __forceinline__ WriteRow write_row_issue(FastDiv hkv, const int64_t* slots, const uint8_t* src,
+                                                    int64_t s_st, int64_t s_sh, uint32_t row) {
+  WriteRow w;
+  w.i = fdiv(row, hkv);
+  w.h = row - w.i * hkv.d;
+  w.slot = slots[w.i];
+  const uint8_t* a = src + w.i * s_st + w.h * s_sh;
+  w.raw[0] = row_load((const u32x4*)a);
+  if constexpr (kSrc == kF32) w.raw[1] = row_load((const u32x4*)(a + 16));
+  return w;
+}
+
+template <int kSrc>
+__device__ __forceinline__ void widen8(const WriteRow& w, float (&x)[8]) {
   if constexpr (kSrc == kF32) {
-    const f32x4 a = row_load((const f32x4*)p);
-    const f32x4 b = row_load((const f32x4*)(p + 16));
-    x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
-    x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t b = w.raw[j >> 2][j & 3];
+      x[j] = u2f(b);
+    }
   } else {
-    raw = row_load((const u32x4*)p);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       // The element goes through a scalar: this compiler lowers
       // __builtin_bit_cast of a vector-element operand to a load from the
       // vector's first element.
-      const uint32_t w = raw[j];
+      const uint32_t b = w.raw[0][j];
       if constexpr (kSrc == kF16) {
-        const f16x2 h = __builtin_bit_cast(f16x2, w);
-        x[2 * j] = (float)h[0];
-        x[2 * j + 1] = (float)h[1];
+        const f16x2 hx = __builtin_bit_cast(f16x2, b);
+        x[2 * j] = (float)hx[0];
+        x[2 * j + 1] = (float)hx[1];
       } else {
-        x[2 * j] = bf16_lo_to_f32(w);
-        x[2 * j + 1] = bf16_hi_to_f32(w);
+        x[2 * j] = bf16_lo_to_f32(b);
+        x[2 * j + 1] = bf16_hi_to_f32(b);
       }
     }
   }
@@ -1733,71 +1753,98 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 }
 
 template <int kSrc, int kPool, bool kScaled>
+__device__ __forceinline__ void write_row_put(const WriteRow& w, uint32_t n_slots, FastDiv page_div, uint8_t* pool,
+                                              int64_t p_sp, int64_t p_sh, int64_t p_st, double rscale) {
+  if (w.slot < 0 || w.slot >= (int64_t)n_slots) return;  // skipped slot
+  const uint32_t page = fdiv((uint32_t)w.slot, page_div);
+  const uint32_t r = (uint32_t)w.slot - page * page_div.d;
+  uint8_t* dst = pool + page * p_sp + w.h * p_sh + r * p_st;
+  if constexpr (kPool == kSrc) {
+    row_store((u32x4*)dst, w.raw[0]);  // same type: a bit-exact copy
+  } else {
+    float x[8];
+    widen8<kSrc>(w, x);
+    if constexpr (kPool == kE4M3) {
+      u32x2 codes{encode_e4m3x4<kScaled>(x, rscale), encode_e4m3x4<kScaled>(x + 4, rscale)};
+      // The NaN fix-up only where the wave holds a NaN: the quantising
+      // write is VALU-bound enough that per-code selects cost it ~2 %.
+      bool nan = false;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) nan = nan || x[j] != x[j];
+      if (__builtin_amdgcn_ballot_w64(nan) != 0) {
+        codes[0] = nan_codes(codes[0], x);
+        codes[1] = nan_codes(codes[1], x + 4);
+      }
+      row_store((u32x2*)dst, codes);
+    } else {
+      row_store((u32x4*)dst, u32x4{pack2<kPool>(x[0], x[1]), pack2<kPool>(x[2], x[3]), pack2<kPool>(x[4], x[5]),
+                                   pack2<kPool>(x[6], x[7])});
+    }
+  }
+}
+
+template <int kSrc, int kPool, bool kScaled>
 __global__ __launch_bounds__(kWriteThreads) void kv_write_kernel(WriteParams p) {
   const int kv = blockIdx.y;
-  if (blockIdx.x == 0 && kv == 0) {
-    for (int j = threadIdx.x; j < p.n_upd; j += kWriteThreads) {
-      const int64_t idx = p.upd[2 * j];
-      if (idx >= 0 && idx < p.bt_numel) p.bt[idx] = (int32_t)p.upd[2 * j + 1];
-    }
+  // The kernel arguments, read in one batch: the asm takes them all in
+  // SGPRs, so their loads go out together and are waited for once, not one
+  // round trip after another behind the branches that first use them.
+  const uint8_t* src0 = p.src[kv];
+  const int64_t s_st = p.s_st[kv], s_sh = p.s_sh[kv];
+  uint8_t* pool0 = p.pool[kv];
+  const int64_t p_sp = p.p_sp[kv], p_sh = p.p_sh[kv], p_st = p.p_st[kv];
+  const float* scale = p.scale[kv];
+  const int64_t* slots = p.slots;
+  const FastDiv hkv = p.hkv, page = p.page, groups = p.groups;
+  const uint32_t n_slots = p.n_slots, rows = p.rows, rows_per_block = p.rows_per_block;
+  const int64_t* upd = p.upd;
+  const int n_upd = p.n_upd;
+  asm volatile("" ::"s"(src0), "s"(s_st), "s"(s_sh), "s"(pool0), "s"(p_sp), "s"(p_sh), "s"(p_st), "s"(scale),
+               "s"(slots), "s"(hkv.m), "s"(hkv.s), "s"(hkv.d), "s"(page.m), "s"(page.s), "s"(page.d),
+               "s"(groups.m), "s"(groups.s), "s"(groups.d), "s"(n_slots), "s"(rows), "s"(rows_per_block), "s"(upd),
+               "s"(n_upd));
+  // Block-table updates (workgroup (0, 0)): the first kWriteThreads are
+  // loaded with the first rows and stored after them, so they add no round
+  // trip to the launch (the decode kernels read both after it ends).
+  const bool upd_block = blockIdx.x == 0 && kv == 0;
+  int64_t upd_idx = -1;
+  int32_t upd_val = 0;
+  if (upd_block && (int)threadIdx.x < n_upd) {
+    upd_idx = upd[2 * threadIdx.x];
+    // (the low word of the int64 value, all the store keeps: a whole-pair
+    // load would leave a dead register the first row's loads wait for)
+    upd_val = ((const int32_t*)upd)[4 * threadIdx.x + 2];
   }
   constexpr int kSrcBytes = (kSrc == kF32) ? 32 : 16;   // 8 source elements
   constexpr int kDstBytes = (kPool == kE4M3) ? 8 : 16;  // 8 pool elements
   // A block covers rows_per_block (token, head) rows per step, `groups`
   // threads per row; the row stride between a thread's steps is fixed, so its
   // column group never changes.
-  const uint32_t groups = p.groups;
-  const uint32_t rows_per_block = kWriteThreads / groups;
-  const uint32_t lrow = threadIdx.x / groups;
-  if (lrow >= rows_per_block) return;
-  const uint32_t g = threadIdx.x - lrow * groups;
-  const uint8_t* src = p.src[kv] + g * kSrcBytes;
-  uint8_t* pool = p.pool[kv] + g * kDstBytes;
-  const int64_t s_st = p.s_st[kv], s_sh = p.s_sh[kv];
-  const int64_t p_sp = p.p_sp[kv], p_sh = p.p_sh[kv], p_st = p.p_st[kv];
-  double rscale = 1.0;
-  if constexpr (kScaled) rscale = 1.0 / (double)*p.scale[kv];
-  const uint32_t step = gridDim.x * rows_per_block;
-  for (uint32_t r0 = blockIdx.x * rows_per_block + lrow; r0 < p.rows; r0 += step * kWriteUnroll) {
-    float x[kWriteUnroll][8];
-    u32x4 raw[kWriteUnroll];
-    int64_t doff[kWriteUnroll];
-#pragma unroll
-    for (int u = 0; u < kWriteUnroll; ++u) {
-      doff[u] = -1;
-      const uint32_t row = r0 + u * step;
-      if (row >= p.rows) continue;
-      const uint32_t i = fdiv(row, p.hkv);
-      const uint32_t h = row - i * p.hkv.d;
-      const int64_t slot = p.slots[i];
-      if (slot < 0 || slot >= (int64_t)p.n_slots) continue;
-      const uint32_t page = fdiv((uint32_t)slot, p.page);
-      const uint32_t r = (uint32_t)slot - page * p.page.d;
-      load8<kSrc>(src + i * s_st + h * s_sh, x[u], raw[u]);
-      doff[u] = page * p_sp + h * p_sh + r * p_st;
+  const uint32_t lrow = fdiv(threadIdx.x, groups);
+  const uint32_t first = blockIdx.x * rows_per_block + lrow;
+  if (lrow < rows_per_block && first < rows) {
+    const uint32_t g = threadIdx.x - lrow * groups.d;
+    const uint8_t* src = src0 + g * kSrcBytes;
+    uint8_t* pool = pool0 + g * kDstBytes;
+    const uint32_t step = gridDim.x * rows_per_block;
+    // The first row's loads go out before the scale's, whose reciprocal
+    // (a binary64 division) the encoding needs only once the row is in.
+    WriteRow w = write_row_issue<kSrc>(hkv, slots, src, s_st, s_sh, first);
+    __builtin_amdgcn_sched_barrier(0);
+    double rscale = 1.0;
+    if constexpr (kScaled) rscale = 1.0 / (double)*scale;
+    for (uint32_t row = first;;) {
+      write_row_put<kSrc, kPool, kScaled>(w, n_slots, page, pool, p_sp, p_sh, p_st, rscale);
+      row += step;
+      if (row >= rows) break;
+      w = write_row_issue<kSrc>(hkv, slots, src, s_st, s_sh, row);
     }
-#pragma unroll
-    for (int u = 0; u < kWriteUnroll; ++u) {
-      if (doff[u] < 0) continue;
-      uint8_t* dst = pool + doff[u];
-      if constexpr (kPool == kE4M3) {
-        u32x2 codes{encode_e4m3x4<kScaled>(x[u], rscale), encode_e4m3x4<kScaled>(x[u] + 4, rscale)};
-        // The NaN fix-up only where the wave holds a NaN: the quantising
-        // write is VALU-bound enough that per-code selects cost it ~2 %.
-        bool nan = false;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) nan = nan || x[u][j] != x[u][j];
-        if (__builtin_amdgcn_ballot_w64(nan) != 0) {
-          codes[0] = nan_codes(codes[0], x[u]);
-          codes[1] = nan_codes(codes[1], x[u] + 4);
-        }
-        row_store((u32x2*)dst, codes);
-      } else if constexpr (kPool == kSrc) {
-        row_store((u32x4*)dst, raw[u]);  // same type: a bit-exact copy
-      } else {
-        row_store((u32x4*)dst, u32x4{pack2<kPool>(x[u][0], x[u][1]), pack2<kPool>(x[u][2], x[u][3]),
-                                     pack2<kPool>(x[u][4], x[u][5]), pack2<kPool>(x[u][6], x[u][7])});
-      }
+  }
+  if (upd_block) {
+    if (upd_idx >= 0 && upd_idx < p.bt_numel) p.bt[upd_idx] = upd_val;
+    for (int j = threadIdx.x + kWriteThreads; j < n_upd; j += kWriteThreads) {
+      const int64_t idx = upd[2 * j];
+      if (idx >= 0 && idx < p.bt_numel) p.bt[idx] = (int32_t)upd[2 * j + 1];
     }
   }
 }
@@ -2382,10 +2429,10 @@ int run_write(const WriteArgs& a) {
   p.rows = (uint32_t)(a.n * a.Hkv);
   p.hkv = make_fastdiv((uint32_t)a.Hkv);
   p.page = make_fastdiv((uint32_t)a.page_size);
-  p.groups = a.D / 8;
+  p.groups = make_fastdiv((uint32_t)(a.D / 8));
+  p.rows_per_block = (uint32_t)(kWriteThreads / (a.D / 8));
   p.bt = a.bt; p.bt_numel = a.bt_numel; p.upd = a.upd; p.n_upd = (int)a.n_upd;
-  const int64_t rows_per_block = kWriteThreads / p.groups;
-  const int64_t blocks = std::min<int64_t>(std::max<int64_t>(cdiv(p.rows, rows_per_block * kWriteUnroll), 1),
+  const int64_t blocks = std::min<int64_t>(std::max<int64_t>(cdiv(p.rows, p.rows_per_block), 1),
                                            (int64_t)device_cus() * FSK_WRITE_BLOCKS_PER_CU);
   const dim3 grid((unsigned)blocks, 2);
   (void)hipGetLastError();
