@@ -1144,6 +1144,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   __builtin_amdgcn_sched_barrier(0);                        // (ahead of any kernel-argument load)
   // ... and while they are in flight, the lane's tile offsets
   const LaneGeo<D, kKV> lg = lane_geo<D, kKV>(p, lane, g, c);
+  // The KV scales, read before the plan's stores (so the compiler knows
+  // nothing in the kernel wrote them and loads them through the scalar
+  // cache) and used after it: their round trip overlaps the lengths'.
+  const float k_scale = kKvFp8 ? p.k_scale[0] : 1.0f;
+  const float v_scale = kKvFp8 ? p.v_scale[0] : 1.0f;
   const Split sp = build_plan<kLayout, kScores>(p, s_pre, s_flat, lane_len, seg_x, lane_flat, lane_pre);
   FSK_STAMP(1);
   int segments_done = 0;
@@ -1161,8 +1166,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   // so each column's scores are its own head's; of the 128 output dims a
   // column keeps its head's half.
   const bool pair = (kLayout == kVarlen && D == 128 && !kScores && !kValu) ? (uniform(p.pair) != 0) : false;
-  const float k_scale = kKvFp8 ? p.k_scale[0] : 1.0f;
-  const float v_scale = kKvFp8 ? p.v_scale[0] : 1.0f;
   const float sscale = p.score_scale * k_scale;
 
   for (int w = blockIdx.x; w < W; w += gridDim.x) {
