@@ -79,6 +79,8 @@ def parse():
     ap.add_argument("--layers", type=int, default=1,
                     help="decode calls per step, over that many independent caches (one decode step of an "
                          "N-layer model); with --graph the whole step is one graph")
+    ap.add_argument("--host-lengths", action="store_true",
+                    help="pass the sequence lengths in host memory (the work plan is built on the host)")
     ap.add_argument("--with-write", action="store_true",
                     help="with --layers: each layer first stores one new token per sequence (KV write kernel)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
@@ -384,14 +386,15 @@ def wave_timeline(args):
     n_sets = args.sets or rotation_sets(base.k.numel() * base.k.element_size() * 2)
     sets = [base] + [W.make(args.config, gen_device=dev, device=dev, data_seed=base.meta["seed"] + 1000 * i)
                      for i in range(1, n_sets)]
+    hl = bool(args.host_lengths)
     for i in range(args.warmup):
-        W.run(sets[i % n_sets], chunk_tokens=args.chunk)
+        W.run(sets[i % n_sets], chunk_tokens=args.chunk, host_lengths=hl)
     n_rec = max(5, min(args.steps, 50))
     # The kernel's own duration: dispatch-stamped events on every call of a
     # separate back-to-back pass (its mean), as in the roofline pass.
     nat.enable_kernel_timing(1)
     for i in range(n_rec):
-        W.run(sets[i % n_sets], chunk_tokens=args.chunk)
+        W.run(sets[i % n_sets], chunk_tokens=args.chunk, host_lengths=hl)
     part_ms, _, n_timed = nat.kernel_timing()
     nat.enable_kernel_timing(0)
     kernel_us = part_ms * 1e3 / max(n_timed, 1)
@@ -405,7 +408,7 @@ def wave_timeline(args):
         # representative: its waves start together, but their first tiles
         # arrive XCD by XCD, up to ~8 µs apart.)
         for i in range(20):
-            W.run(sets[(r + i) % n_sets], chunk_tokens=args.chunk)
+            W.run(sets[(r + i) % n_sets], chunk_tokens=args.chunk, host_lengths=hl)
         torch.cuda.synchronize()
         buf = np.zeros(4096 * 16, dtype=np.uint64)
         nat.check(lib.fsk_debug_wave_stamps(buf.ctypes.data, 4096))
@@ -809,7 +812,8 @@ def main():
         for j in range(g * L, g * L + L):
             if writes is not None:
                 W.run_write(writes[j])
-            out = W.run(sets[j], chunk_tokens=args.chunk, block_scores=args.block_scores)
+            out = W.run(sets[j], chunk_tokens=args.chunk, block_scores=args.block_scores,
+                        host_lengths=args.host_lengths)
         return out
 
     n_groups = n_sets // L
@@ -888,6 +892,7 @@ def main():
             "block_scores": bool(args.block_scores),
             "layers": L,
             "with_write": bool(args.with_write),
+            "host_lengths": bool(args.host_lengths),
             "us_per_call": round(ms_step * 1e3 / L, 2),
         },
         "roofline": {

@@ -272,6 +272,22 @@ struct Params {
   int nblk;
 };
 
+// A plan built on the host (the host-plan entry points, for callers that
+// hold the sequence lengths in host memory): the split and each sequence's
+// tables, exactly as build_plan computes them on the device, passed in the
+// kernel arguments.  Entries past B hold flat[B] and pre[B].
+constexpr int kHostPlanMax = FSK_HOST_PLAN_MAX_BATCH;  // most sequences of a host-planned call
+struct HostPlan {
+  int32_t c_e, c_o, n, paired;
+  uint32_t m;
+  int32_t seg_x;
+  int32_t pre_end;              // pre[B]: the call's partials
+  int32_t len[kHostPlanMax];    // sequence lengths (clamped as seq_range does)
+  int32_t start[kHostPlanMax];  // first row of each sequence (varlen, dense)
+  int32_t flat[kHostPlanMax];   // stream offset of each sequence's region
+  int32_t pre[kHostPlanMax];    // first partial of each sequence
+};
+
 // Token range [start, start+len) of sequence b in its layout's row space.
 template <int kLayout>
 __device__ __forceinline__ void seq_range(const Params& p, int b, int& start, int& len) {
@@ -1099,9 +1115,16 @@ __device__ __forceinline__ void compute_tile_valu(const TileRegs<D, kF16>& T, ui
 // Waves per SIMD the register budget is sized for (2: <= 256 VGPRs).
 constexpr int kWavesPerEu = FSK_PIPE_DEPTH > 2 ? 1 : 2;
 
-template <int D, int kQ, int kKV, int kLayout, bool kScores, bool kValu = false>
+// The host's plan, when a launch passes one (after the Params).
+__device__ __forceinline__ const HostPlan* plan_ptr() { return nullptr; }
+__device__ __forceinline__ const HostPlan* plan_ptr(const HostPlan& h) { return &h; }
+
+// The partial kernel.  Plan: none (the kernel builds the plan on the device
+// from the lengths) or a HostPlan (built by the host from host lengths,
+// B <= kHostPlanMax; lens_arg and starts_arg are then unused).
+template <int D, int kQ, int kKV, int kLayout, bool kScores, bool kValu = false, typename... Plan>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu))) void partial_kernel(
-    const int32_t* lens_arg, const int32_t* starts_arg, int B_arg, Params pk) {
+    const int32_t* lens_arg, const int32_t* starts_arg, int B_arg, Params pk, Plan... host_plan) {
   // The plan's first loads (the lengths) need only these three, which lead
   // the argument list so that the dispatch preloads them into SGPRs
   // (-amdgpu-kernarg-preload-count): the length loads issue without waiting
@@ -1110,6 +1133,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   p.lens = lens_arg;
   p.starts = starts_arg;
   p.B = B_arg;
+  constexpr bool kHostPlan = sizeof...(Plan) == 1;
+  const HostPlan* hp = plan_ptr(host_plan...);
   using TR = TileRegs<D, kKV>;
   using SM = Softmax<D, kQ, kKV>;
   constexpr bool kKvFp8 = TR::kFp8;
@@ -1121,6 +1146,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   static_assert(kKV != kF16 || kQ != kBF16, "f16 KV needs f16 Q");
   static_assert(!kValu || (D == 128 && kQ == kF16 && kKV == kF16 && !kScores && kLayout != kDense),
                 "the VALU tile is built for f16, D = 128, paged and varlen");
+  static_assert(!kHostPlan || (!kScores && !kValu), "host plans are for the plain decode kernels");
 
   __shared__ __attribute__((aligned(16))) uint8_t s_kstage_mem[kDepth * 2 * TR::kHalfBytes];
   // LDS offset of the stage = low 32 bits of its generic address
@@ -1140,16 +1166,42 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   int lane_start, lane_len;  // start and length of sequence `lane` (B <= 64)
   int lane_flat, lane_pre;   // flat[lane] and pre[lane] of the plan (B <= 64)
   int seg_x;  // empty stream positions before each sequence (see build_plan)
-  seq_range_first<kLayout>(p, lane, lane_start, lane_len);  // the wave's first memory requests
-  __builtin_amdgcn_sched_barrier(0);                        // (ahead of any kernel-argument load)
+  Split sp;
+  if constexpr (kHostPlan) {
+    // The host's plan: each lane's entries from the kernel arguments (one
+    // round trip), the split from scalar loads.
+    lane_len = hp->len[lane];
+    lane_start = hp->start[lane];
+    lane_flat = hp->flat[lane];
+    lane_pre = hp->pre[lane];
+    __builtin_amdgcn_sched_barrier(0);
+    sp.c_e = hp->c_e;
+    sp.c_o = hp->c_o;
+    sp.pair = sp.c_e + sp.c_o;
+    sp.n = hp->n;
+    sp.paired = hp->paired;
+    sp.m = hp->m;
+    seg_x = hp->seg_x;
+  } else {
+    seq_range_first<kLayout>(p, lane, lane_start, lane_len);  // the wave's first memory requests
+    __builtin_amdgcn_sched_barrier(0);                        // (ahead of any kernel-argument load)
+  }
   // ... and while they are in flight, the lane's tile offsets
   const LaneGeo<D, kKV> lg = lane_geo<D, kKV>(p, lane, g, c);
-  // The KV scales, read before the plan's stores (so the compiler knows
-  // nothing in the kernel wrote them and loads them through the scalar
-  // cache) and used after it: their round trip overlaps the lengths'.
+  // The KV scales, read before the plan (their round trip overlaps the
+  // lengths') and used after it.
   const float k_scale = kKvFp8 ? p.k_scale[0] : 1.0f;
   const float v_scale = kKvFp8 ? p.v_scale[0] : 1.0f;
-  const Split sp = build_plan<kLayout, kScores>(p, s_pre, s_flat, lane_len, seg_x, lane_flat, lane_pre);
+  if constexpr (kHostPlan) {
+    // Workgroup 0 publishes the unit prefix for the reduce kernel, as
+    // build_plan does (lanes past B hold pre[B]).
+    if (blockIdx.x == 0) {
+      if (lane < p.B) p.plan[lane] = lane_pre;
+      if (lane == 0) p.plan[p.B] = hp->pre_end;
+    }
+  } else {
+    sp = build_plan<kLayout, kScores>(p, s_pre, s_flat, lane_len, seg_x, lane_flat, lane_pre);
+  }
   FSK_STAMP(1);
   int segments_done = 0;
   const int NH = p.n_items_h;
@@ -1390,6 +1442,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu)
   FSK_STAMP_AT(5, (unsigned long long)segments_done);
   FSK_STAMP(4);
   (void)segments_done;
+  (void)hp;
 }
 
 // ---------------------------------------------------------------------------
@@ -2071,6 +2124,7 @@ struct Common {
   hipStream_t stream;
   void* scores; int nblk;  // block scores [B, Hq, nblk] in the output dtype, or null
   bool no_timing;          // never stamp this call (no event creation: the allocation-free entry)
+  bool lens_on_host;       // lens is host memory: the plan is built here (make_host_plan)
 };
 
 bool aligned(const void* p, int a) { return ((uintptr_t)p % a) == 0; }
@@ -2176,6 +2230,29 @@ int dispatch_qkv(const Params& p, int grid, int q_dt, int kv_dt, const Launch& s
   return FSK_OK;
 }
 
+template <int D, int kQ, int kKV, int kLayout>
+void launch_partial_hp(const Params& p, const HostPlan& hp, int grid, const Launch& s) {
+  launch(partial_kernel<D, kQ, kKV, kLayout, false, false, HostPlan>, dim3(grid), dim3(64), 0, s,
+         (const int32_t*)nullptr, (const int32_t*)nullptr, p.B, p, hp);
+}
+
+template <int D, int kLayout>
+int dispatch_qkv_hp(const Params& p, const HostPlan& hp, int grid, int q_dt, int kv_dt, const Launch& s) {
+  if (kv_dt == FSK_F16) launch_partial_hp<D, kF16, kF16, kLayout>(p, hp, grid, s);
+  else if (kv_dt == FSK_BF16) launch_partial_hp<D, kBF16, kBF16, kLayout>(p, hp, grid, s);
+  else if (q_dt == FSK_F16) launch_partial_hp<D, kF16, kE4M3, kLayout>(p, hp, grid, s);
+  else if (q_dt == FSK_BF16) launch_partial_hp<D, kBF16, kE4M3, kLayout>(p, hp, grid, s);
+  else return fail(FSK_ERR_UNSUPPORTED, "e4m3 q only on the dense layout");
+  return FSK_OK;
+}
+
+template <int D>
+int dispatch_layout_hp(int layout, const Params& p, const HostPlan& hp, int grid, int q_dt, int kv_dt,
+                       const Launch& s) {
+  return layout == FSK_LAYOUT_VARLEN ? dispatch_qkv_hp<D, kVarlen>(p, hp, grid, q_dt, kv_dt, s)
+                                     : dispatch_qkv_hp<D, kPaged>(p, hp, grid, q_dt, kv_dt, s);
+}
+
 // The VALU-tile kernels (option qk_engine = 1; f16, D = 128, paged or varlen).
 int launch_valu(int layout, const Params& p, int grid, const Launch& s) {
   if (layout == FSK_LAYOUT_PAGED)
@@ -2246,6 +2323,66 @@ SplitArgs make_split_args(int chunk_min, int chunk_max, int chunk_pref, int targ
   return a;
 }
 
+// The plan build_plan computes on the device, computed here from host
+// lengths (varlen: cu_seqlens [B+1]; paged: seq_lens [B]) with the same
+// clamps, split rule (split_geometry, chunk_of) and prefix sums, so a
+// host-planned call does exactly what the device-planned one does.
+int make_host_plan(const Common& c, const Params& p, HostPlan& hp) {
+  if (c.B > kHostPlanMax)
+    return fail(FSK_ERR_UNSUPPORTED, "host lengths: at most " + std::to_string(kHostPlanMax) + " sequences a call");
+  memset(&hp, 0, sizeof(hp));
+  auto clampi = [](int x, int lo, int hi) { return x < lo ? lo : (x > hi ? hi : x); };
+  constexpr int kA = 32;  // stream padding of the plain decode kernels
+  uint32_t total = 0;     // < 2^31 - 4096: validate bounds the stream
+  int nonempty = 0, ref = -1;
+  bool varied = false;
+  for (int b = 0; b < c.B; ++b) {
+    int start = 0, len;
+    if (c.layout == FSK_LAYOUT_VARLEN) {
+      start = clampi(c.lens[b], 0, p.kv_extent);
+      len = clampi(c.lens[b + 1], start, p.kv_extent) - start;
+    } else {
+      len = clampi(c.lens[b], 0, p.max_blocks * p.page_size);
+    }
+    hp.start[b] = start;
+    hp.len[b] = len;
+    total += (uint32_t)((len + kA - 1) / kA * kA);
+    if (len > 0) {
+      ++nonempty;
+      if (ref < 0) ref = len;
+      varied = varied || len != ref;
+    }
+  }
+  const uint32_t seg = (uint32_t)p.seg_tokens;
+  int X = 0;
+  Split sp;
+  if (seg > 0 && varied) {
+    sp = split_geometry(total + (uint32_t)nonempty * seg, p.split, kA);
+    if (sp.n <= 8 * nonempty || (uint32_t)sp.c_e <= seg) X = (int)seg;
+    else sp = split_geometry(total, p.split, kA);
+  } else {
+    sp = split_geometry(total, p.split, kA);
+  }
+  int carry_f = 0, carry_u = 0;
+  for (int b = 0; b < c.B; ++b) {
+    const int len = hp.len[b];
+    const int fs = carry_f + X;  // the sequence's first token in the stream
+    const int n = len > 0 ? chunk_of(sp, fs + len - 1) - chunk_of(sp, fs) + 1 : 0;
+    hp.flat[b] = carry_f;
+    hp.pre[b] = std::min(carry_u, p.u_max);
+    carry_f += (len + kA - 1) / kA * kA + (len > 0 ? X : 0);
+    carry_u += n;
+  }
+  for (int b = c.B; b < kHostPlanMax; ++b) {
+    hp.flat[b] = carry_f;
+    hp.pre[b] = std::min(carry_u, p.u_max);
+  }
+  hp.pre_end = std::min(carry_u, p.u_max);
+  hp.c_e = sp.c_e; hp.c_o = sp.c_o; hp.n = sp.n; hp.paired = sp.paired; hp.m = sp.m;
+  hp.seg_x = X;
+  return FSK_OK;
+}
+
 int run_decode(const Common& c) {
   int st = validate(c);
   if (st != FSK_OK) return st;
@@ -2313,6 +2450,14 @@ int run_decode(const Common& c) {
                 c.layout != FSK_LAYOUT_DENSE))
     return fail(FSK_ERR_UNSUPPORTED, "qk_engine 1 (VALU tile) covers f16 q and KV, head_dim 128, at most 4 query "
                                      "heads per KV head, the paged and varlen layouts and no block scores");
+  HostPlan hp;
+  if (c.lens_on_host) {
+    if (c.scores || valu || c.layout == FSK_LAYOUT_DENSE)
+      return fail(FSK_ERR_UNSUPPORTED, "host lengths: paged and varlen decode without block scores");
+    st = make_host_plan(c, p, hp);
+    if (st != FSK_OK) return st;
+    p.lens = nullptr;  // (host memory: the kernel takes the plan instead)
+  }
 
   // Workgroups that can find a work item: no more than the workspace holds,
   // nor than the split can plan (a grid of 8 per CU for 4 items per CU made
@@ -2332,7 +2477,11 @@ int run_decode(const Common& c) {
   int rc;
   const bool sc = c.scores != nullptr;
   const Launch lp{c.stream, ev[0], ev[1]};
-  if (valu) rc = launch_valu(c.layout, p, grid, lp);
+  if (c.lens_on_host) {
+    if (c.D == 64 && !pair) rc = dispatch_layout_hp<64>(c.layout, p, hp, grid, c.q_dt, c.kv_dt, lp);
+    else if (c.D <= 128) rc = dispatch_layout_hp<128>(c.layout, p, hp, grid, c.q_dt, c.kv_dt, lp);
+    else rc = dispatch_layout_hp<256>(c.layout, p, hp, grid, c.q_dt, c.kv_dt, lp);
+  } else if (valu) rc = launch_valu(c.layout, p, grid, lp);
   else if (c.D == 64 && !pair) rc = dispatch_layout<64>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
   else if (c.D <= 128) rc = dispatch_layout<128>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
   else rc = dispatch_layout<256>(c.layout, sc, p, grid, c.q_dt, c.kv_dt, lp);
@@ -2626,20 +2775,23 @@ int fsk_decode_paged_scores(const void* q, int64_t q_stride_b, int64_t q_stride_
   return run_decode(c);
 }
 
-int fsk_decode_varlen(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k, int64_t k_stride_t,
-                      int64_t k_stride_h, const void* v, int64_t v_stride_t, int64_t v_stride_h,
-                      const int32_t* cu_seqlens, int64_t total_tokens, const float* s_aux, int sink_mode,
-                      const float* k_scale, const float* v_scale, void* out, int64_t o_stride_b,
-                      int64_t o_stride_h, int batch, int num_q_heads, int num_kv_heads, int head_dim, int q_dtype,
-                      int kv_dtype, int out_dtype, float sm_scale, void* workspace, int64_t workspace_bytes,
-                      int chunk_tokens, void* stream) {
+}  // extern "C"
+
+namespace {
+int decode_varlen(bool host_lens, const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
+                  int64_t k_stride_t, int64_t k_stride_h, const void* v, int64_t v_stride_t, int64_t v_stride_h,
+                  const int32_t* cu_seqlens, int64_t total_tokens, const float* s_aux, int sink_mode,
+                  const float* k_scale, const float* v_scale, void* out, int64_t o_stride_b, int64_t o_stride_h,
+                  int batch, int num_q_heads, int num_kv_heads, int head_dim, int q_dtype, int kv_dtype,
+                  int out_dtype, float sm_scale, void* workspace, int64_t workspace_bytes, int chunk_tokens,
+                  void* stream) {
   Common c;
   memset(&c, 0, sizeof(c));
   c.layout = FSK_LAYOUT_VARLEN;
   c.q = q; c.q_sb = q_stride_b; c.q_sh = q_stride_h;
   c.k = k; c.k_st = k_stride_t; c.k_sh = k_stride_h;
   c.v = v; c.v_st = v_stride_t; c.v_sh = v_stride_h;
-  c.lens = cu_seqlens; c.kv_extent = total_tokens;
+  c.lens = cu_seqlens; c.kv_extent = total_tokens; c.lens_on_host = host_lens;
   c.s_aux = s_aux; c.sink_mode = sink_mode; c.k_scale = k_scale; c.v_scale = v_scale;
   c.out = out; c.o_sb = o_stride_b; c.o_sh = o_stride_h;
   c.B = batch; c.Hq = num_q_heads; c.Hkv = num_kv_heads; c.D = head_dim;
@@ -2648,14 +2800,14 @@ int fsk_decode_varlen(const void* q, int64_t q_stride_b, int64_t q_stride_h, con
   return run_decode(c);
 }
 
-int fsk_decode_paged(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_pool, int64_t k_stride_p,
-                     int64_t k_stride_h, int64_t k_stride_t, const void* v_pool, int64_t v_stride_p,
-                     int64_t v_stride_h, int64_t v_stride_t, const int32_t* block_table, int64_t bt_stride_b,
-                     int max_blocks, const int32_t* seq_lens, int num_pages, int page_size, const float* s_aux,
-                     int sink_mode, const float* k_scale, const float* v_scale, void* out, int64_t o_stride_b,
-                     int64_t o_stride_h, int batch, int num_q_heads, int num_kv_heads, int head_dim, int q_dtype,
-                     int kv_dtype, int out_dtype, float sm_scale, void* workspace, int64_t workspace_bytes,
-                     int chunk_tokens, void* stream) {
+int decode_paged(bool host_lens, const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_pool,
+                 int64_t k_stride_p, int64_t k_stride_h, int64_t k_stride_t, const void* v_pool, int64_t v_stride_p,
+                 int64_t v_stride_h, int64_t v_stride_t, const int32_t* block_table, int64_t bt_stride_b,
+                 int max_blocks, const int32_t* seq_lens, int num_pages, int page_size, const float* s_aux,
+                 int sink_mode, const float* k_scale, const float* v_scale, void* out, int64_t o_stride_b,
+                 int64_t o_stride_h, int batch, int num_q_heads, int num_kv_heads, int head_dim, int q_dtype,
+                 int kv_dtype, int out_dtype, float sm_scale, void* workspace, int64_t workspace_bytes,
+                 int chunk_tokens, void* stream) {
   Common c;
   memset(&c, 0, sizeof(c));
   c.layout = FSK_LAYOUT_PAGED;
@@ -2664,6 +2816,7 @@ int fsk_decode_paged(const void* q, int64_t q_stride_b, int64_t q_stride_h, cons
   c.v = v_pool; c.v_s0 = v_stride_p; c.v_sh = v_stride_h; c.v_st = v_stride_t;
   c.bt = block_table; c.bt_sb = bt_stride_b; c.max_blocks = max_blocks;
   c.lens = seq_lens; c.num_pages = num_pages; c.page_size = page_size; c.kv_extent = max_blocks;
+  c.lens_on_host = host_lens;
   c.s_aux = s_aux; c.sink_mode = sink_mode; c.k_scale = k_scale; c.v_scale = v_scale;
   c.out = out; c.o_sb = o_stride_b; c.o_sh = o_stride_h;
   c.B = batch; c.Hq = num_q_heads; c.Hkv = num_kv_heads; c.D = head_dim;
@@ -2671,6 +2824,38 @@ int fsk_decode_paged(const void* q, int64_t q_stride_b, int64_t q_stride_h, cons
   c.ws = workspace; c.ws_bytes = workspace_bytes; c.chunk = chunk_tokens; c.stream = (hipStream_t)stream;
   return run_decode(c);
 }
+}  // namespace
+
+extern "C" {
+
+#define FSK_VARLEN_PARAMS                                                                                          \
+  const void *q, int64_t q_stride_b, int64_t q_stride_h, const void *k, int64_t k_stride_t, int64_t k_stride_h,   \
+      const void *v, int64_t v_stride_t, int64_t v_stride_h, const int32_t *cu_seqlens, int64_t total_tokens,     \
+      const float *s_aux, int sink_mode, const float *k_scale, const float *v_scale, void *out, int64_t o_stride_b, \
+      int64_t o_stride_h, int batch, int num_q_heads, int num_kv_heads, int head_dim, int q_dtype, int kv_dtype,   \
+      int out_dtype, float sm_scale, void *workspace, int64_t workspace_bytes, int chunk_tokens, void *stream
+#define FSK_VARLEN_ARGS                                                                                            \
+  q, q_stride_b, q_stride_h, k, k_stride_t, k_stride_h, v, v_stride_t, v_stride_h, cu_seqlens, total_tokens, s_aux, \
+      sink_mode, k_scale, v_scale, out, o_stride_b, o_stride_h, batch, num_q_heads, num_kv_heads, head_dim,        \
+      q_dtype, kv_dtype, out_dtype, sm_scale, workspace, workspace_bytes, chunk_tokens, stream
+#define FSK_PAGED_PARAMS                                                                                           \
+  const void *q, int64_t q_stride_b, int64_t q_stride_h, const void *k_pool, int64_t k_stride_p,                  \
+      int64_t k_stride_h, int64_t k_stride_t, const void *v_pool, int64_t v_stride_p, int64_t v_stride_h,         \
+      int64_t v_stride_t, const int32_t *block_table, int64_t bt_stride_b, int max_blocks, const int32_t *seq_lens, \
+      int num_pages, int page_size, const float *s_aux, int sink_mode, const float *k_scale,                      \
+      const float *v_scale, void *out, int64_t o_stride_b, int64_t o_stride_h, int batch, int num_q_heads,        \
+      int num_kv_heads, int head_dim, int q_dtype, int kv_dtype, int out_dtype, float sm_scale, void *workspace,  \
+      int64_t workspace_bytes, int chunk_tokens, void *stream
+#define FSK_PAGED_ARGS                                                                                             \
+  q, q_stride_b, q_stride_h, k_pool, k_stride_p, k_stride_h, k_stride_t, v_pool, v_stride_p, v_stride_h,          \
+      v_stride_t, block_table, bt_stride_b, max_blocks, seq_lens, num_pages, page_size, s_aux, sink_mode, k_scale, \
+      v_scale, out, o_stride_b, o_stride_h, batch, num_q_heads, num_kv_heads, head_dim, q_dtype, kv_dtype,         \
+      out_dtype, sm_scale, workspace, workspace_bytes, chunk_tokens, stream
+
+int fsk_decode_varlen(FSK_VARLEN_PARAMS) { return decode_varlen(false, FSK_VARLEN_ARGS); }
+int fsk_decode_varlen_host(FSK_VARLEN_PARAMS) { return decode_varlen(true, FSK_VARLEN_ARGS); }
+int fsk_decode_paged(FSK_PAGED_PARAMS) { return decode_paged(false, FSK_PAGED_ARGS); }
+int fsk_decode_paged_host(FSK_PAGED_PARAMS) { return decode_paged(true, FSK_PAGED_ARGS); }
 
 }  // extern "C"
 

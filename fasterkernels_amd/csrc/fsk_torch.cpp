@@ -93,6 +93,24 @@ at::Tensor int32_contig(const at::Tensor& t, const char* name, const c10::Device
 
 const void* ptr_or_null(const c10::optional<at::Tensor>& t) { return t && t->defined() ? t->data_ptr() : nullptr; }
 
+// Sequence lengths: a device tensor, or host memory (then the work plan is
+// built on the host: the *_host entry points).  Host lengths that the host
+// path does not take (block scores, more than FSK_HOST_PLAN_MAX_BATCH
+// sequences) are copied to the device instead.
+struct Lengths {
+  at::Tensor t;
+  bool host;
+};
+Lengths lengths(const at::Tensor& t, const char* name, const c10::Device& dev, bool host_ok) {
+  if (!t.defined()) raise(FSK_ERR_INVALID, std::string(name) + " is undefined");
+  if (t.is_cuda()) return {int32_contig(t, name, dev), false};
+  if (t.device().type() != c10::kCPU)
+    raise(kRuntime, std::string(name) + " must be on the GPU or in host memory, got " + t.device().str());
+  const at::Tensor h = t.to(at::kInt).contiguous();
+  if (host_ok) return {h, true};
+  return {h.to(dev), false};
+}
+
 c10::optional<at::Tensor> sinks(const c10::optional<at::Tensor>& s, int64_t hq, const c10::Device& dev) {
   if (!s || !s->defined()) return c10::nullopt;
   on_device(*s, "s_aux", dev);
@@ -173,7 +191,9 @@ at::Tensor paged(const at::Tensor& q_in, const at::Tensor& k_pool, const at::Ten
   if (block_table.dim() != 2 || block_table.size(0) < B) raise(FSK_ERR_INVALID, "block_table must be [batch, max_blocks]");
   at::Tensor bt = block_table.scalar_type() == at::kInt ? block_table : block_table.to(at::kInt);
   if (bt.stride(1) != 1) bt = bt.contiguous();
-  const at::Tensor lens = int32_contig(seq_lens, "seq_lens", dev);
+  const bool with_scores_arg = scores && scores->defined();
+  const Lengths ln = lengths(seq_lens, "seq_lens", dev, !with_scores_arg && B <= FSK_HOST_PLAN_MAX_BATCH);
+  const at::Tensor& lens = ln.t;
   if (lens.numel() < B) raise(FSK_ERR_INVALID, "seq_lens must have one entry per sequence");
   const auto sk = sinks(s_aux, Hq, dev);
   const auto ks = scale(k_scale, "k_scale", dev), vs = scale(v_scale, "v_scale", dev);
@@ -197,7 +217,8 @@ at::Tensor paged(const at::Tensor& q_in, const at::Tensor& k_pool, const at::Ten
   const float* vsp = static_cast<const float*>(ptr_or_null(vs));
   int st;
   if (!with_scores) {
-    st = fsk_decode_paged(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+    auto entry = ln.host ? fsk_decode_paged_host : fsk_decode_paged;
+    st = entry(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
                           k.stride(2), v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), bt.data_ptr<int32_t>(),
                           bt.stride(0), (int)max_blocks, lens.data_ptr<int32_t>(), (int)P, (int)PS, sp,
                           (int)sink_mode, ksp, vsp, out.data_ptr(), out.stride(0), out.stride(1), (int)B, (int)Hq,
@@ -232,7 +253,9 @@ at::Tensor varlen(const at::Tensor& q_in, const at::Tensor& k_varlen, const at::
   const int64_t B = q.size(0), Hq = q.size(1), D = q.size(2);
   const int64_t T = k.size(0), Hkv = k.size(1);
   if (v.sizes() != k.sizes() || k.size(2) != D) raise(FSK_ERR_INVALID, "k_varlen / v_varlen shapes disagree with q");
-  const at::Tensor cu = int32_contig(cu_seqlens_k, "cu_seqlens_k", dev);
+  const bool with_scores_arg = scores && scores->defined();
+  const Lengths ln = lengths(cu_seqlens_k, "cu_seqlens_k", dev, !with_scores_arg && B <= FSK_HOST_PLAN_MAX_BATCH);
+  const at::Tensor& cu = ln.t;
   if (cu.numel() != B + 1)
     raise(FSK_ERR_INVALID, "cu_seqlens_k must have batch+1=" + std::to_string(B + 1) + " entries");
   const auto sk = sinks(s_aux, Hq, dev);
@@ -255,7 +278,8 @@ at::Tensor varlen(const at::Tensor& q_in, const at::Tensor& k_varlen, const at::
   const float* vsp = static_cast<const float*>(ptr_or_null(vs));
   int st;
   if (!with_scores) {
-    st = fsk_decode_varlen(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+    auto entry = ln.host ? fsk_decode_varlen_host : fsk_decode_varlen;
+    st = entry(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
                            v.data_ptr(), v.stride(0), v.stride(1), cu.data_ptr<int32_t>(), T, sp, (int)sink_mode, ksp,
                            vsp, out.data_ptr(), out.stride(0), out.stride(1), (int)B, (int)Hq, (int)Hkv, (int)D, qd,
                            kd, od, scl, ws.data_ptr(), nbytes, (int)chunk_tokens, stream_ptr(stream));

@@ -48,6 +48,11 @@ SIGNATURES = {
     "fsk_decode_paged": (_I, [_P, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _I, _P, _I, _I,
                               _P, _I, _P, _P, _P, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _P, _L,
                               _I, _P]),
+    "fsk_decode_varlen_host": (_I, [_P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _P, _I, _P, _P,
+                                    _P, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _P, _L, _I, _P]),
+    "fsk_decode_paged_host": (_I, [_P, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _I, _P, _I, _I,
+                                   _P, _I, _P, _P, _P, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _P, _L,
+                                   _I, _P]),
     "fsk_decode_paged_noalloc": (_I, [_P, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _I, _P, _I, _I,
                                       _P, _I, _P, _P, _P, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P]),
     "fsk_decode_dense": (_I, [_P, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _L, _P, _P, _P, _I, _P,

@@ -82,6 +82,19 @@ class Workload:
     def total_tokens(self) -> int:
         return int(sum(self.lens))
 
+    def host_lengths(self) -> torch.Tensor:
+        """The lengths in host memory, as the host-plan entry points take them
+        (paged: seq_lens [B]; varlen: cu_seqlens [B+1]); made once."""
+        if "_host_lengths" not in self.meta:
+            lens = torch.tensor(self.lens, dtype=torch.int64)
+            if self.layout == "paged":
+                t = lens.to(torch.int32)
+            else:
+                t = torch.zeros(self.B + 1, dtype=torch.int32)
+                t[1:] = torch.cumsum(lens, 0).to(torch.int32)
+            self.meta["_host_lengths"] = t
+        return self.meta["_host_lengths"]
+
     def to(self, device) -> "Workload":
         def mv(t):
             return None if t is None else t.to(device)
@@ -210,16 +223,21 @@ def reference_sweep_workload(B: int, S: int, *, device=None, gen_device=None, da
                 overrides=dict(B=B, lens=("uniform", max(64, S // 4), S), sinks=True, sink_scale=0.1))
 
 
-def run(wl: Workload, *, sink_mode: str = "exp", chunk_tokens: int = 0, block_scores: bool = False):
+def run(wl: Workload, *, sink_mode: str = "exp", chunk_tokens: int = 0, block_scores: bool = False,
+        host_lengths: bool = False):
     """One decode step of ``wl`` through the HIP entry points (with
-    ``block_scores``: also the pooled block scores, returned as (out, S))."""
+    ``block_scores``: also the pooled block scores, returned as (out, S); with
+    ``host_lengths``: the lengths passed in host memory, so the work plan is
+    built on the host)."""
     from fskernels.hip import decode as dec
     if wl.layout == "paged":
-        return dec.paged_flash_decode(wl.q, wl.k, wl.v, wl.block_table, wl.seq_lens, PAGE,
+        lens = wl.host_lengths() if host_lengths else wl.seq_lens
+        return dec.paged_flash_decode(wl.q, wl.k, wl.v, wl.block_table, lens, PAGE,
                                       s_aux=wl.s_aux, k_scale=wl.k_scale, v_scale=wl.v_scale,
                                       out_dtype=wl.out_dtype, sink_mode=sink_mode,
                                       chunk_tokens=chunk_tokens, return_block_scores=block_scores)
-    return dec.flash_decode_gqa_varlen(wl.q, wl.k, wl.v, wl.cu_seqlens, wl.s_aux,
+    cu = wl.host_lengths() if host_lengths else wl.cu_seqlens
+    return dec.flash_decode_gqa_varlen(wl.q, wl.k, wl.v, cu, wl.s_aux,
                                        sink_mode=sink_mode, k_scale=wl.k_scale, v_scale=wl.v_scale,
                                        out_dtype=wl.out_dtype, chunk_tokens=chunk_tokens,
                                        return_block_scores=block_scores)

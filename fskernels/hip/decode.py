@@ -154,6 +154,10 @@ def flash_decode_gqa_varlen(q, k_varlen, v_varlen, cu_seqlens_k, s_aux=None, *,
     CUDA/TileLang variants fskernels/cuda/cuda_fd_gqa.py:14-15,
     fskernels/tilelang/tilelang_gqa_decode.py:135-172).  q [B, Hq, D];
     k_varlen / v_varlen [T, Hkv, D] packed by cu_seqlens_k int32 [B+1];
+    cu_seqlens_k may be a host (CPU) tensor: the work plan is then built on
+    the host from it (no device read of the lengths at the start of every
+    workgroup; bit-identical results), for up to 64 sequences without block
+    scores, and copied to the device otherwise.
     s_aux fp32 [Hq] sinks folded per ``sink_mode``: "linear" (default) adds
     the sink to the softmax denominator relative to the running maximum, as
     all three replaced kernels do (triton_gqa_decode.py:112-115,
@@ -243,8 +247,12 @@ def paged_flash_decode(q, k_pool, v_pool, block_table, seq_lens, page_size, *, s
     Reference: fskernels/paged_attn/triton_paged_attn.py:96-125.  q [B, Hq, D];
     k_pool / v_pool [P, Hkv, page_size, D] (e.g. PagedKVCache.k_pool[layer]);
     block_table int32 [B, max_blocks] (logical page -> physical page, entries
-    past a sequence's last page are never read); seq_lens int32 [B].  The
-    keyword-only arguments add sinks and fp8 (e4m3) pools with per-tensor
+    past a sequence's last page are never read); seq_lens int32 [B], on the
+    GPU or in host memory (``PagedKVCache.get_seq_lens_tensor(ids,
+    device="cpu")``): host lengths let the work plan be built on the host (no
+    device read of the lengths at the start of every workgroup;
+    bit-identical results), for up to 64 sequences without block scores, and
+    are copied to the device otherwise.  The keyword-only arguments add sinks and fp8 (e4m3) pools with per-tensor
     scales, which the reference kernel does not have, and the block scores of
     flash_decode_gqa_varlen (default width: the block table's token capacity).
     """

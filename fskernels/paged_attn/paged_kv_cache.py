@@ -321,10 +321,13 @@ class PagedKVCache:
         idx = torch.tensor(active_seq_ids, dtype=torch.long, device=self.device)
         return self.block_table[idx]
 
-    def get_seq_lens_tensor(self, active_seq_ids: List[int]) -> torch.Tensor:
-        """int32 [n] lengths on the cache's device (:139-141)."""
+    def get_seq_lens_tensor(self, active_seq_ids: List[int], *, device=None) -> torch.Tensor:
+        """int32 [n] lengths on the cache's device (:139-141), or on ``device``
+        (keyword-only addition): ``device="cpu"`` gives host lengths, which
+        ``paged_flash_decode`` takes as they are and builds its work plan
+        from on the host, with no copy to the GPU."""
         lens = [self._seq_lens[sid] for sid in active_seq_ids]
-        return torch.tensor(lens, dtype=torch.int32, device=self.device)
+        return torch.tensor(lens, dtype=torch.int32, device=self.device if device is None else device)
 
     # ------------------------------------------------------------------
     @property

@@ -129,6 +129,47 @@ FSK_API int fsk_decode_paged(const void *q, int64_t q_stride_b, int64_t q_stride
                      void *workspace, int64_t workspace_bytes, int chunk_tokens,
                      void *stream);
 
+/* Varlen and paged decode with the lengths in host memory: cu_seqlens
+ * (int32 [B+1]) / seq_lens (int32 [B]) are HOST pointers, read during the
+ * call; everything else as fsk_decode_varlen / fsk_decode_paged, with the
+ * same results bit for bit.  The work plan that the device-length entry
+ * points build on the GPU from the lengths (a memory round trip and the
+ * split's arithmetic at the start of every workgroup) is built here on the
+ * host and passed in the kernel arguments.  For callers that already hold
+ * the lengths on the host: a serving loop (PagedKVCache keeps them, as the
+ * reference's does, fskernels/paged_attn/paged_kv_cache.py:59, :139-141),
+ * and the reference's own varlen bindings, which copy cu_seqlens to the host
+ * on every call (fskernels/cuda/flash_decode_api.cpp:22,
+ * fskernels/triton/triton_gqa_decode.py:135).  No block scores; at most 64
+ * sequences (FSK_ERR_UNSUPPORTED beyond).  Under HIP-graph capture the plan
+ * is captured with the call: a replay decodes the captured lengths. */
+FSK_API int fsk_decode_varlen_host(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                      const void *k, int64_t k_stride_t, int64_t k_stride_h,
+                      const void *v, int64_t v_stride_t, int64_t v_stride_h,
+                      const int32_t *cu_seqlens, int64_t total_tokens,
+                      const float *s_aux, int sink_mode,
+                      const float *k_scale, const float *v_scale,
+                      void *out, int64_t o_stride_b, int64_t o_stride_h,
+                      int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                      int q_dtype, int kv_dtype, int out_dtype, float sm_scale,
+                      void *workspace, int64_t workspace_bytes, int chunk_tokens,
+                      void *stream);
+FSK_API int fsk_decode_paged_host(const void *q, int64_t q_stride_b, int64_t q_stride_h,
+                     const void *k_pool, int64_t k_stride_p, int64_t k_stride_h,
+                     int64_t k_stride_t,
+                     const void *v_pool, int64_t v_stride_p, int64_t v_stride_h,
+                     int64_t v_stride_t,
+                     const int32_t *block_table, int64_t bt_stride_b, int max_blocks,
+                     const int32_t *seq_lens, int num_pages, int page_size,
+                     const float *s_aux, int sink_mode,
+                     const float *k_scale, const float *v_scale,
+                     void *out, int64_t o_stride_b, int64_t o_stride_h,
+                     int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                     int q_dtype, int kv_dtype, int out_dtype, float sm_scale,
+                     void *workspace, int64_t workspace_bytes, int chunk_tokens,
+                     void *stream);
+#define FSK_HOST_PLAN_MAX_BATCH 64
+
 /* Allocation-free paged decode.  No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under HIP-graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and

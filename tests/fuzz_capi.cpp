@@ -30,6 +30,12 @@ static void* pick_p() {
     default: return (void*)0x7f0000001000ULL;
   }
 }
+// Host lengths for the *_host entry points (host memory, read by the call).
+static int32_t host_lens[65];
+static const int32_t* pick_host_lens() {
+  for (int i = 0; i < 65; ++i) host_lens[i] = rng() % 3 ? (int32_t)(rng() % 70000) : (int32_t)pick_i();
+  return host_lens;
+}
 static void check(int st, const char* fn) {
   if (st > 0 || st < -4) { printf("%s returned %d\n", fn, st); }
   const char* e = fsk_last_error();
@@ -57,6 +63,17 @@ int main() {
                            (const float*)pick_p(), (const float*)pick_p(), pick_p(), pick_i64(), pick_i64(), pick_i(),
                            pick_i(), pick_i(), pick_i(), pick_i() & 3, pick_i() & 3, pick_i() & 3, 0.1f, pick_p(),
                            pick_i64(), pick_i(), nullptr), "paged");
+    check(fsk_decode_varlen_host(pick_p(), pick_i64(), pick_i64(), pick_p(), pick_i64(), pick_i64(), pick_p(),
+                                 pick_i64(), pick_i64(), pick_host_lens(), pick_i64(), (const float*)pick_p(), pick_i(),
+                                 (const float*)pick_p(), (const float*)pick_p(), pick_p(), pick_i64(), pick_i64(),
+                                 (int)(rng() % 70) - 2, pick_i(), pick_i(), pick_i(), pick_i() & 3, pick_i() & 3,
+                                 pick_i() & 3, 0.1f, pick_p(), pick_i64(), pick_i(), nullptr), "varlen-host");
+    check(fsk_decode_paged_host(pick_p(), pick_i64(), pick_i64(), pick_p(), pick_i64(), pick_i64(), pick_i64(),
+                                pick_p(), pick_i64(), pick_i64(), pick_i64(), (const int32_t*)pick_p(), pick_i64(),
+                                pick_i(), pick_host_lens(), pick_i(), pick_i(), (const float*)pick_p(), pick_i(),
+                                (const float*)pick_p(), (const float*)pick_p(), pick_p(), pick_i64(), pick_i64(),
+                                (int)(rng() % 70) - 2, pick_i(), pick_i(), pick_i(), pick_i() & 3, pick_i() & 3,
+                                pick_i() & 3, 0.1f, pick_p(), pick_i64(), pick_i(), nullptr), "paged-host");
     check(fsk_decode_dense(pick_p(), pick_i64(), pick_i64(), pick_p(), pick_i64(), pick_i64(), pick_i64(), pick_p(),
                            pick_i64(), pick_i64(), pick_i64(), pick_i64(), (const int32_t*)pick_p(),
                            (const int32_t*)pick_p(), (const float*)pick_p(), pick_i(), (const float*)pick_p(),
@@ -87,6 +104,14 @@ int main() {
                            (const float*)a[17], (int)a[18], (const float*)a[19], (const float*)a[20], (void*)a[21],
                            a[22], a[23], (int)a[24], (int)a[25], (int)a[26], (int)a[27], (int)a[28], (int)a[29],
                            (int)a[30], 0.088f, (void*)a[32], a[33], (int)a[34], nullptr), "paged-perturbed");
+    // the same arguments with host lengths (valid host memory, random values)
+    if ((int)a[24] >= 0 && (int)a[24] <= 65)
+      check(fsk_decode_paged_host((void*)a[0], a[1], a[2], (void*)a[3], a[4], a[5], a[6], (void*)a[7], a[8], a[9],
+                                  a[10], (const int32_t*)a[11], a[12], (int)a[13], pick_host_lens(), (int)a[15],
+                                  (int)a[16], (const float*)a[17], (int)a[18], (const float*)a[19],
+                                  (const float*)a[20], (void*)a[21], a[22], a[23], (int)a[24], (int)a[25],
+                                  (int)a[26], (int)a[27], (int)a[28], (int)a[29], (int)a[30], 0.088f, (void*)a[32],
+                                  a[33], (int)a[34], nullptr), "paged-host-perturbed");
     (void)fsk_workspace_bytes((int)(rng() % 4), (int)a[24], (int)a[25], (int)a[26], (int)a[27], (a[13] & 0xFFFFFF) * 16,
                               (int)a[16], (int)a[34]);
   }

@@ -59,6 +59,8 @@ def test_plan_matches_reference_bookkeeping():
         assert slots == [page * 16 + pos % 16]
     assert c.block_table[s].tolist() == ref.block_table[s].tolist() == [7, 6, 5, -1]
     assert c.get_seq_lens_tensor([s]).tolist() == [33]
+    host = c.get_seq_lens_tensor([s], device="cpu")
+    assert host.device.type == "cpu" and host.dtype == torch.int32 and host.tolist() == [33]
     assert c.pages_used == 3
 
 
