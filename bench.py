@@ -909,6 +909,12 @@ def main():
         },
         "cpu_baseline": None,
     }
+    if args.host_lengths:
+        # Measured: the dispatch-stamped events read host-plan launches as long
+        # as (or longer than) device-length ones, while the steps, the kernel
+        # traces of rocprofv3 and the wave stamps all show them ~1 µs shorter.
+        out["roofline"]["note"] = ("dispatch-stamped events do not resolve host-plan launches: use the step time "
+                                   "or a rocprofv3 kernel trace for the partial kernel")
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(sets[0], args.cpu_seconds)
     del sets, base, writes
