@@ -69,6 +69,29 @@ def test_host_lengths_bit_identical(name, ov, mode, chunk):
     assert_same(d, h, f"{name} {ov} {mode} chunk {chunk}")
 
 
+@pytest.mark.parametrize("seed", range(60))
+def test_host_lengths_random_configurations(seed):
+    """The decode suite's random configurations (layout, dtypes, head
+    grouping and dim, batch, lengths with zeros and page-boundary values,
+    sinks, split size; test_gpu_decode.py::_random_case), both sink modes."""
+    from tests.test_gpu_decode import _random_case
+    name, ov, chunk = _random_case(5000 + seed)
+    wl = W.make(name, overrides=ov, seed=seed).to(DEV)
+    d, h = both(wl, chunk_tokens=chunk, sink_mode=("exp", "linear")[seed % 2])
+    assert_same(d, h, f"seed {seed}: {name} {ov} chunk={chunk}")
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_host_lengths_random_large_batches(seed):
+    """The suite's random large batches (9-300 sequences): up to 64 on the
+    host path, the rest through the device copy."""
+    from tests.test_gpu_decode import _random_large_case
+    name, ov, chunk = _random_large_case(7000 + seed)
+    wl = W.make(name, overrides=ov, seed=seed, gen_device=DEV, device=DEV)
+    d, h = both(wl, chunk_tokens=chunk)
+    assert_same(d, h, f"large seed {seed}: {name} B={ov['B']} chunk={chunk}")
+
+
 @pytest.mark.parametrize("name", ["M0", "C1", "C2", "C4"])
 def test_host_lengths_benchmark_sizes(name):
     """The benchmark configurations at their stated sizes (B = 4)."""
