@@ -31,8 +31,10 @@ decode configurations, C1..C5, the same way and adds them under ``configs``:
 each with its own warm-up and step count set from elapsed time (about 0.3 s
 of each, stated in the entry), its partial kernel's roofline (with the
 counter traffic of profiles/partial_kernel_<config>_traffic.md) and a CPU
-baseline of about 3 s.  ``--configs C2,C4`` picks others, ``--configs ''``
-none.  ``--sweep`` runs only the reference benchmark's own sweep
+baseline of about 3 s; then C1 and C4 again with their lengths passed in host
+memory (``C1:host``, ``C4:host``: the opt-in host-plan path, step times; the
+dispatch-stamped kernel timing does not resolve those launches).
+``--configs C2,C4`` picks others, ``--configs ''`` none.  ``--sweep`` runs only the reference benchmark's own sweep
 (benchmarks/benchmark.py:20-33, 150-158: varlen fp16, lengths uniform in
 [max(64, S/4), S], sinks 0.1 N(0,1) folded linearly; S = 512..32768 at B=4
 and B = 1..32 at S=16384), one JSON line per point.
@@ -566,7 +568,10 @@ def graph_host(args) -> None:
 # other decode configurations of the benchmark definition).  Each gets its own
 # warm-up and step count, set from elapsed time (the headline keeps the counts
 # the command line gives), and a bounded CPU-baseline budget.
-SUB_CONFIGS = ("C1", "C2", "C3", "C4", "C5")
+SUB_CONFIGS = ("C1", "C2", "C3", "C4", "C5", "C1:host", "C4:host")
+# "<config>:host": the same workload with its lengths passed in host memory
+# (the host-plan entry points; an opt-in of this build, the drop-in path keeps
+# device lengths).
 SUB_WARMUP_S = 0.3    # warm-up: at least this long (and at least 50 steps in all)
 SUB_TIMED_S = 0.3     # timed steps: about this long (100 to 5000 steps)
 SUB_CPU_S = 3.0       # CPU-baseline budget per configuration (seconds)
@@ -653,7 +658,7 @@ def workload_name(config: str, wl) -> str:
 
 
 def measure_decode(sets, *, sink_mode: str = "exp", warm_s: float = SUB_WARMUP_S,
-                   timed_s: float = SUB_TIMED_S) -> dict:
+                   timed_s: float = SUB_TIMED_S, host_lengths: bool = False) -> dict:
     """Step and kernel timing of eager decode calls over rotating input sets,
     with a time-based warm-up and step count (see time_based_counts)."""
     from fasterkernels_amd import native as nat
@@ -661,7 +666,7 @@ def measure_decode(sets, *, sink_mode: str = "exp", warm_s: float = SUB_WARMUP_S
     n_sets = len(sets)
 
     def step(i):
-        return W.run(sets[i % n_sets], sink_mode=sink_mode)
+        return W.run(sets[i % n_sets], sink_mode=sink_mode, host_lengths=host_lengths)
 
     warmup, steps, est = time_based_counts(step, warm_s, timed_s)
     elapsed, issued, med_us = timed_pass(step, steps, warmup - 20)
@@ -717,12 +722,21 @@ def sub_config(config: str, dev, cpu_seconds: float, no_cpu: bool) -> dict:
     HBM-resident inputs, eager decode calls, the partial kernel timed by its
     own dispatches), with a time-based warm-up and step count."""
     t_start = time.perf_counter()
-    sets = decode_sets(config, dev)
-    m = measure_decode(sets)
-    entry = {"workload": workload_name(config, sets[0]),
+    base_name, _, mode = config.partition(":")
+    host = mode == "host"
+    sets = decode_sets(base_name, dev)
+    m = measure_decode(sets, host_lengths=host)
+    entry = {"workload": workload_name(base_name, sets[0]) + (", lengths in host memory" if host else ""),
              "sinks": None if sets[0].s_aux is None else "N(0,1), exp fold (sink logit)", **m}
-    entry["roofline"]["traffic"] = read_traffic(traffic_path(config))
-    entry["cpu_baseline"] = None if no_cpu else cpu_baseline(sets[0], cpu_seconds)
+    if host:
+        entry["roofline"]["traffic"] = None
+        entry["roofline"]["note"] = ("dispatch-stamped events do not resolve host-plan launches: use the step time "
+                                     "or a rocprofv3 kernel trace for the partial kernel")
+        entry["cpu_baseline"] = None
+        entry["cpu_baseline_note"] = f"the same workload as {base_name}'s entry"
+    else:
+        entry["roofline"]["traffic"] = read_traffic(traffic_path(base_name))
+        entry["cpu_baseline"] = None if no_cpu else cpu_baseline(sets[0], cpu_seconds)
     release(sets)
     entry["wall_s"] = round(time.perf_counter() - t_start, 2)
     return entry
@@ -928,7 +942,8 @@ def main():
         torch.cuda.empty_cache()
         out["configs"] = {}
         for name in subs:
-            if name not in W.CONFIGS:
+            base_name, _, mode = name.partition(":")
+            if base_name not in W.CONFIGS or mode not in ("", "host"):
                 raise SystemExit(f"--configs: unknown decode configuration {name!r}")
             print(f"# timing {name}", file=sys.stderr, flush=True)
             out["configs"][name] = sub_config(name, dev, SUB_CPU_S, args.no_cpu)
