@@ -765,8 +765,9 @@ def reference_sweep(args) -> None:
         n_sets = rotation_sets(base.k.numel() * base.k.element_size() * 2)
         sets = [base] + [W.reference_sweep_workload(B, S, gen_device=dev, device=dev, data_seed=4200 + i)
                          for i in range(1, n_sets)]
-        m = measure_decode(sets, sink_mode="linear")
-        row = {"sweep": kind, "B": B, "max_S": S, "lens": list(base.lens), **m}
+        m = measure_decode(sets, sink_mode="linear", host_lengths=args.host_lengths)
+        row = {"sweep": kind, "B": B, "max_S": S, "lens": list(base.lens), "host_lengths": bool(args.host_lengths),
+               **m}
         release(sets)
         rows.append(row)
         print(json.dumps(row), flush=True)
