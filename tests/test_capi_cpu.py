@@ -164,6 +164,33 @@ def test_paged_validation(lib, override, code):
     assert lib.fsk_last_error()  # a message explains the status
 
 
+def test_host_length_entries(lib):
+    """The host-length entry points validate like the device-length ones,
+    read the lengths from host memory, refuse more than 64 sequences, and
+    otherwise reach the launch (which fails here, without a GPU, with the
+    device-length entry's status)."""
+    lens = (ctypes.c_int32 * 65)(*([100] * 65))
+    host = ctypes.cast(lens, ctypes.c_void_p).value
+    assert lib.fsk_decode_paged_host(*paged_args(lens=None)) == nat.FSK_ERR_INVALID
+    assert lib.fsk_decode_paged_host(*paged_args(lens=host, D=96)) == nat.FSK_ERR_UNSUPPORTED
+    assert lib.fsk_decode_paged_host(*paged_args(lens=host, B=65)) == nat.FSK_ERR_UNSUPPORTED
+    assert b"64" in lib.fsk_last_error()
+    want = lib.fsk_decode_paged(*paged_args())
+    assert want != nat.FSK_OK
+    assert lib.fsk_decode_paged_host(*paged_args(lens=host)) == want
+    assert lib.fsk_decode_paged_host(*paged_args(lens=host, B=64)) == want
+    cu = (ctypes.c_int32 * 65)(*range(0, 650, 10))
+    ok = [FAKE, 32 * 128, 128, FAKE, 8 * 128, 128, FAKE, 8 * 128, 128, ctypes.cast(cu, ctypes.c_void_p).value,
+          1000, None, 0, None, None, FAKE, 32 * 128, 128, 4, 32, 8, 128, nat.FSK_F16, nat.FSK_F16, nat.FSK_F16,
+          0.088, FAKE, 1 << 30, 0, None]
+    dev = list(ok)
+    dev[9] = FAKE
+    assert lib.fsk_decode_varlen_host(*ok) == lib.fsk_decode_varlen(*dev) != nat.FSK_OK
+    bad = list(ok)
+    bad[18] = 65
+    assert lib.fsk_decode_varlen_host(*bad) == nat.FSK_ERR_UNSUPPORTED
+
+
 def test_varlen_and_dense_validation(lib):
     ok = [FAKE, 32 * 128, 128, FAKE, 8 * 128, 128, FAKE, 8 * 128, 128, FAKE, 1000, None, 0, None, None,
           FAKE, 32 * 128, 128, 4, 32, 8, 128, nat.FSK_F16, nat.FSK_F16, nat.FSK_F16, 0.088, FAKE, 1 << 30, 0,
