@@ -11,6 +11,9 @@
 //      query head.  The work list is built by every workgroup from the
 //      sequence lengths (a wave prefix scan into LDS), so the host never reads
 //      lengths back and the grid size only depends on host-known bounds.
+//      When the caller holds the lengths in host memory (the *_host entry
+//      points), the host builds the same work list and passes it in the
+//      kernel arguments instead (HostPlan).
 //   2. reduce_kernel: one 256-thread workgroup per (sequence, query head) combines the
 //      partials with a log-sum-exp merge, folds the attention sink and writes
 //      the output in the requested dtype.
